@@ -1,0 +1,129 @@
+/*
+ * nativebit_amd.h -- C ABI of libnativebit_amd.so, the MI355X (gfx950)
+ * packed-weight decode path for NativeBit codebook-quantized layers.
+ *
+ * Data format (identical to the reference, byte for byte):
+ *   - weights W (N x K, row major) are split into flat blocks of
+ *     `block_size` consecutive weights: block j covers flat elements
+ *     [j*block_size, (j+1)*block_size) of W.reshape(-1); the last block is
+ *     zero padded.  num_blocks = ceil(N*K / block_size).
+ *     (nativebit/layers.py:43-50)
+ *   - codebook: float32 [num_blocks][n_entries], row major.
+ *   - packed indices: one index per (padded) weight, bits = ceil(log2
+ *     n_entries), written LSB first into a little-endian bit stream: index i
+ *     occupies stream bits [i*bits, (i+1)*bits).  3-bit streams are padded
+ *     to whole 24-bit groups (3 bytes per 8 indices), others to whole bytes.
+ *     (nativebit/pack.py:21-138, inference/pack.py:38-57,
+ *      inference/triton_kernel.py:199-220)
+ *   - dequantized weight: W.flat[i] = codebook[i / block_size][index i].
+ *     (nativebit/pack.py:145-169, inference/triton_kernel.py:268-273)
+ *
+ * Conventions:
+ *   - Every function returns 0 (NB_OK) or a negative nb_status.  Argument
+ *     checks run on the host before anything is launched, so they can be
+ *     exercised without a GPU; nb_last_error() gives a thread-local message.
+ *   - Device pointers are caller-owned; the library never allocates device
+ *     memory and never synchronizes.  Work is enqueued on `stream` (a
+ *     hipStream_t; NULL = the default stream) and is graph-capturable.
+ *   - Element types are passed as nb_dtype codes; activations x and outputs
+ *     y may be NB_F32 or NB_BF16.  Arithmetic: weights are the exact fp32
+ *     codebook values, x is widened to fp32, products and sums are fp32
+ *     (nb_gemm_prefill: weights and x rounded to bf16, fp32 accumulation).
+ */
+#ifndef NATIVEBIT_AMD_H
+#define NATIVEBIT_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NB_ABI_VERSION 1
+
+enum nb_status {
+    NB_OK = 0,
+    NB_EINVAL = -1,        /* bad argument: null pointer, negative size, ... */
+    NB_EUNSUPPORTED = -2,  /* valid format the library has no kernel for      */
+    NB_EALIGN = -3,        /* pointer not aligned to its element type         */
+    NB_ELAUNCH = -4,       /* the HIP runtime refused the launch              */
+    NB_ENODEV = -5         /* no usable gfx950 device                         */
+};
+
+enum nb_dtype {
+    NB_F32 = 0,
+    NB_BF16 = 1,
+    NB_U8 = 2
+};
+
+/* Version of this ABI (NB_ABI_VERSION of the build). */
+int nb_abi_version(void);
+
+/* Message for the last non-zero status returned on this thread. */
+const char* nb_last_error(void);
+
+/* Bytes of a packed stream of `count` indices of `bits` bits (0 if bits is
+ * out of 1..8).  Mirrors the padding of nativebit/pack.py:29-32 (3-bit) and
+ * 105-107 (others). */
+int64_t nb_packed_nbytes(int64_t count, int bits);
+
+/*
+ * Fused dequant + matvec / skinny GEMM:
+ *     y[m][n] = sum_k x[m][k] * W[n][k],   0 <= m < M, 0 <= n < N.
+ * x: M rows of K elements, row stride ldx (elements); y: M rows of N
+ * elements, row stride ldy.  M in 1..16.  bits in 1..8 with
+ * n_entries <= 2^bits; any N, K >= 0 and block_size >= 1.  Indices >=
+ * n_entries (never produced by the packers) read the last entry.
+ *
+ * Replaces: dequant_matvec_3bit(x, packed, codebook, N, K)
+ *           (inference/cuda_kernel.py:84-104, 133-136),
+ *           dequant_matvec_3bit(x, packed_indices, codebook, N, K)
+ *           (inference/triton_kernel.py:186-196),
+ *           dequant_matvec(x, indices, codebook, N, K) with bits = 8
+ *           (inference/triton_kernel.py:119-140),
+ *           and PackedLinear.forward for x_flat.shape[0] <= 16
+ *           (inference/triton_kernel.py:240-275).
+ */
+int nb_gemv(const void* x, int x_dtype, int64_t ldx,
+            const uint8_t* packed, const float* codebook,
+            void* y, int y_dtype, int64_t ldy,
+            int M, int N, int K, int bits, int n_entries, int block_size,
+            void* stream);
+
+/*
+ * Unpack `count` indices of `bits` bits to one byte each.
+ * Replaces: unpack_3bit / unpack_4bit / unpack_nbits
+ *           (nativebit/pack.py:44-68, 85-90, 119-138) and
+ *           unpack_indices_3bit (inference/generate_torch.py:165-173).
+ */
+int nb_unpack(const uint8_t* packed, uint8_t* idx_out, int64_t count, int bits,
+              void* stream);
+
+/*
+ * Pack `count` one-byte indices (low `bits` bits used) into the stream,
+ * writing exactly nb_packed_nbytes(count, bits) bytes (padding zero).
+ * Replaces: pack_indices_to_3bit (inference/triton_kernel.py:199-220),
+ *           pack_3bit / pack_4bit / pack_nbits (nativebit/pack.py:21-116),
+ *           pack_indices_3bit (inference/pack.py:38-57).
+ */
+int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits,
+            void* stream);
+
+/*
+ * Dequantize the first `total` weights: w[i] = codebook[i / block_size][index
+ * i], written as float32 (exact copy) or bfloat16 (round to nearest even, as
+ * torch's .to(torch.bfloat16)).  num_blocks * block_size must be >= total.
+ * Replaces: reconstruct_weight (nativebit/pack.py:145-169) and the gather of
+ *           PackedLinear's batched branch (inference/triton_kernel.py:260-273),
+ *           NativeBitInferenceLinear.forward (nativebit/inference.py:42-46).
+ */
+int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out,
+               int w_dtype, int64_t total, int64_t num_blocks, int bits,
+               int n_entries, int block_size, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NATIVEBIT_AMD_H */

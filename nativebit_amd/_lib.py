@@ -1,0 +1,95 @@
+"""ctypes binding of libnativebit_amd.so (the C ABI in include/nativebit_amd.h).
+
+torch is imported before the library is opened so that the library's
+libamdhip64 dependency resolves to the HIP runtime torch already loaded (one
+runtime per process: torch's streams and pointers are valid in our calls).
+
+There is no fallback: if the library is missing, or a call returns a non-zero
+status, a NativeBitError is raised with the library's own message.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (must be loaded first, see module docstring)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libnativebit_amd.so")
+
+NB_OK = 0
+NB_EINVAL = -1
+NB_EUNSUPPORTED = -2
+NB_EALIGN = -3
+NB_ELAUNCH = -4
+NB_ENODEV = -5
+STATUS_NAMES = {
+    NB_EINVAL: "NB_EINVAL", NB_EUNSUPPORTED: "NB_EUNSUPPORTED",
+    NB_EALIGN: "NB_EALIGN", NB_ELAUNCH: "NB_ELAUNCH", NB_ENODEV: "NB_ENODEV",
+}
+
+NB_F32 = 0
+NB_BF16 = 1
+NB_U8 = 2
+
+ABI_VERSION = 1
+
+# Every symbol include/nativebit_amd.h declares: (name, restype, argtypes).
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_L = ctypes.c_int64
+SIGNATURES = {
+    "nb_abi_version": (_I, []),
+    "nb_last_error": (ctypes.c_char_p, []),
+    "nb_packed_nbytes": (_L, [_L, _I]),
+    "nb_gemv": (_I, [_P, _I, _L, _P, _P, _P, _I, _L, _I, _I, _I, _I, _I, _I, _P]),
+    "nb_unpack": (_I, [_P, _P, _L, _I, _P]),
+    "nb_pack": (_I, [_P, _P, _L, _I, _P]),
+    "nb_dequant": (_I, [_P, _P, _P, _I, _L, _L, _I, _I, _I, _P]),
+}
+
+
+class NativeBitError(RuntimeError):
+    """A non-zero status from libnativebit_amd.so."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        super().__init__(f"{STATUS_NAMES.get(status, status)}: {message}")
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def load():
+    """Opens the library once and declares every exported signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} not found: build it with `python -m nativebit_amd.build` "
+                "(the HIP path has no CPU fallback)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.nb_abi_version() != ABI_VERSION:
+            raise ImportError(f"{LIB_PATH}: ABI {lib.nb_abi_version()} != {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != NB_OK:
+        msg = load().nb_last_error().decode(errors="replace")
+        raise NativeBitError(status, msg)
+
+
+def last_error() -> str:
+    return load().nb_last_error().decode(errors="replace")

@@ -1,0 +1,100 @@
+"""PackedLinear: drop-in for the reference's packed NativeBit linear layer.
+
+Mirrors inference/triton_kernel.py:223-286: the same buffers
+(``packed_indices`` flat uint8 stream, ``codebook`` (num_blocks, n_entries)
+float32), the same ``out_features`` / ``in_features`` attributes, the same
+``from_packed(indices_np, codebook_np, weight_shape, device)`` constructor and
+a ``forward`` that takes any leading dimensions and returns float32 by
+default.  Differences, all deliberate:
+
+* every row count runs on the gfx950 kernels of libnativebit_amd.so (the
+  reference uses a CUDA kernel for one row and torch unpack+gather+matmul for
+  more); nothing falls back silently -- a failure raises NativeBitError
+  (the reference swallows every exception, triton_kernel.py:252);
+* bit width, entries per block and block size are attributes (defaults 3, 8
+  and 128, the reference's constants, triton_kernel.py:18-19);
+* ``out_dtype`` may be bfloat16 for callers that keep activations in bf16.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import ops
+
+BS = 128  # weights per codebook block (inference/triton_kernel.py:18)
+NE = 8    # codebook entries per block (inference/triton_kernel.py:19)
+
+MAX_GEMV_ROWS = 16
+
+
+class PackedLinear(torch.nn.Module):
+    """y = x @ W.T with W held as packed indices + per-block codebooks."""
+
+    def __init__(self, packed_indices: torch.Tensor, codebook: torch.Tensor,
+                 out_features: int, in_features: int, block_size: int = BS,
+                 bits: int | None = None, out_dtype: torch.dtype = torch.float32):
+        super().__init__()
+        self.register_buffer("packed_indices", packed_indices)  # flat uint8 stream
+        self.register_buffer("codebook", codebook)              # (num_blocks, n_entries)
+        self.out_features = int(out_features)
+        self.in_features = int(in_features)
+        self.block_size = int(block_size)
+        self.n_entries = int(codebook.shape[1])
+        self.bits = int(bits) if bits is not None else ops.bits_for_entries(self.n_entries)
+        self.out_dtype = out_dtype
+        total = self.out_features * self.in_features
+        need_blocks = -(-total // self.block_size)
+        if codebook.shape[0] != need_blocks:
+            raise ValueError(f"codebook has {codebook.shape[0]} blocks; "
+                             f"{self.out_features}x{self.in_features} at block "
+                             f"{self.block_size} needs {need_blocks}")
+        need = ops.packed_nbytes(need_blocks * self.block_size, self.bits)
+        if packed_indices.numel() < ops.packed_nbytes(total, self.bits):
+            raise ValueError(f"packed_indices has {packed_indices.numel()} bytes, "
+                             f"expected {need}")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        shape = x.shape
+        if x.dim() == 0 or shape[-1] != self.in_features:
+            raise ValueError(f"x last dim must be {self.in_features}, got {tuple(shape)}")
+        x_flat = x.reshape(-1, self.in_features)
+        if x_flat.dtype not in (torch.float32, torch.bfloat16):
+            x_flat = x_flat.to(torch.float32)
+        M = x_flat.shape[0]
+        y = torch.empty((M, self.out_features), dtype=self.out_dtype, device=x.device)
+        for m0 in range(0, M, MAX_GEMV_ROWS):
+            m1 = min(M, m0 + MAX_GEMV_ROWS)
+            ops.gemv(x_flat[m0:m1], self.packed_indices, self.codebook,
+                     self.out_features, self.in_features, bits=self.bits,
+                     block_size=self.block_size, out_dtype=self.out_dtype,
+                     out=y[m0:m1])
+        return y.reshape(*shape[:-1], self.out_features)
+
+    @staticmethod
+    def from_packed(indices_np, codebook_np, weight_shape, device="cuda",
+                    block_size: int = BS) -> "PackedLinear":
+        """Build from unpacked uint8 indices (as read from a .nbpack.npz).
+
+        Like the reference (triton_kernel.py:277-286) the indices are moved to
+        the device and packed there (nb_pack kernel).
+        """
+        idx = torch.from_numpy(np.ascontiguousarray(indices_np, dtype=np.uint8)).to(device)
+        cb = torch.from_numpy(np.ascontiguousarray(codebook_np, dtype=np.float32)).to(device)
+        bits = ops.bits_for_entries(cb.shape[1])
+        packed = ops.pack(idx, bits)
+        return PackedLinear(packed, cb, int(weight_shape[0]), int(weight_shape[1]),
+                            block_size=block_size, bits=bits)
+
+    @staticmethod
+    def from_stream(packed_np, codebook_np, weight_shape, device="cuda",
+                    block_size: int = BS, bits: int | None = None) -> "PackedLinear":
+        """Build directly from an already-packed stream (no unpack/repack)."""
+        packed = torch.from_numpy(np.ascontiguousarray(packed_np, dtype=np.uint8)).to(device)
+        cb = torch.from_numpy(np.ascontiguousarray(codebook_np, dtype=np.float32)).to(device)
+        return PackedLinear(packed, cb, int(weight_shape[0]), int(weight_shape[1]),
+                            block_size=block_size, bits=bits)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bits={self.bits}, n_entries={self.n_entries}, block_size={self.block_size}")

@@ -1,0 +1,134 @@
+"""The C ABI without a GPU: the library loads, exports exactly what
+include/nativebit_amd.h declares, and rejects bad arguments on the host
+before any launch (no compute call is made here).
+
+Pointers passed below are never dereferenced: every call either fails
+validation or has nothing to do (N == 0 / count == 0).
+"""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from nativebit_amd import _lib
+from tests.conftest import ROOT, gpu_available
+
+HEADER = os.path.join(ROOT, "include", "nativebit_amd.h")
+FAKE = 0x100000  # aligned, never dereferenced
+
+
+def declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(nb_[a-z_0-9]+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert declared() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH],
+                         capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r" T (nb_\w+)$", out, flags=re.M))
+    assert declared() <= exported
+    for name in declared():
+        assert getattr(lib, name) is not None
+    assert lib.nb_abi_version() == 1
+
+
+def test_packed_nbytes(golden):
+    lib = _lib.load()
+    for e in golden["lengths"]:
+        assert lib.nb_packed_nbytes(e["count"], e["bits"]) == e["nbytes"]
+    assert lib.nb_packed_nbytes(10, 0) == 0 and lib.nb_packed_nbytes(10, 9) == 0
+
+
+def gemv(**kw):
+    a = dict(x=FAKE, x_dtype=_lib.NB_F32, ldx=0, packed=FAKE, codebook=FAKE, y=FAKE,
+             y_dtype=_lib.NB_F32, ldy=0, M=1, N=8, K=256, bits=3, n_entries=8,
+             block_size=128, stream=None)
+    a.update(kw)
+    return _lib.load().nb_gemv(*a.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(M=0), _lib.NB_EUNSUPPORTED),
+    (dict(M=17), _lib.NB_EUNSUPPORTED),
+    (dict(N=-1), _lib.NB_EINVAL),
+    (dict(bits=0), _lib.NB_EUNSUPPORTED),
+    (dict(bits=9), _lib.NB_EUNSUPPORTED),
+    (dict(n_entries=9), _lib.NB_EINVAL),
+    (dict(n_entries=0), _lib.NB_EINVAL),
+    (dict(block_size=0), _lib.NB_EINVAL),
+    (dict(x_dtype=7), _lib.NB_EINVAL),
+    (dict(y_dtype=_lib.NB_U8), _lib.NB_EINVAL),
+    (dict(M=2, ldx=100), _lib.NB_EINVAL),
+    (dict(M=2, ldx=256, ldy=4), _lib.NB_EINVAL),
+    (dict(y=None), _lib.NB_EINVAL),
+    (dict(packed=None), _lib.NB_EINVAL),
+    (dict(codebook=None), _lib.NB_EINVAL),
+    (dict(y=FAKE + 2), _lib.NB_EALIGN),
+    (dict(x=FAKE + 1, x_dtype=_lib.NB_BF16), _lib.NB_EALIGN),
+    (dict(codebook=FAKE + 2), _lib.NB_EALIGN),
+])
+def test_gemv_validation(kw, status):
+    assert gemv(**kw) == status
+    assert _lib.last_error()  # a message for every failure
+
+
+def test_gemv_empty_is_noop():
+    assert gemv(N=0, y=None, x=None) == _lib.NB_OK
+
+
+def test_codec_validation():
+    lib = _lib.load()
+    assert lib.nb_unpack(FAKE, FAKE, 10, 9, None) == _lib.NB_EUNSUPPORTED
+    assert lib.nb_unpack(FAKE, FAKE, -1, 3, None) == _lib.NB_EINVAL
+    assert lib.nb_unpack(None, FAKE, 10, 3, None) == _lib.NB_EINVAL
+    assert lib.nb_unpack(None, None, 0, 3, None) == _lib.NB_OK
+    assert lib.nb_pack(FAKE, None, 10, 3, None) == _lib.NB_EINVAL
+    assert lib.nb_pack(FAKE, FAKE, 10, 0, None) == _lib.NB_EUNSUPPORTED
+    dq = lib.nb_dequant
+    assert dq(FAKE, FAKE, FAKE, _lib.NB_F32, 1000, 7, 3, 8, 128, None) == _lib.NB_EINVAL
+    assert dq(FAKE, FAKE, FAKE, _lib.NB_U8, 100, 1, 3, 8, 128, None) == _lib.NB_EINVAL
+    assert dq(FAKE, FAKE + 1, FAKE, _lib.NB_F32, 100, 1, 3, 8, 128, None) == _lib.NB_EALIGN
+    assert dq(FAKE, FAKE, FAKE + 1, _lib.NB_BF16, 100, 1, 3, 8, 128, None) == _lib.NB_EALIGN
+    assert dq(FAKE, FAKE, FAKE, _lib.NB_F32, 100, 1, 3, 9, 128, None) == _lib.NB_EINVAL
+    assert dq(None, None, None, _lib.NB_F32, 0, 0, 3, 8, 128, None) == _lib.NB_OK
+
+
+@pytest.mark.skipif(gpu_available(), reason="only meaningful without a GPU")
+def test_valid_call_without_gpu_reports_nodev():
+    # All arguments valid: validation passes and the device check refuses.
+    assert gemv() == _lib.NB_ENODEV
+    assert "gfx950" in _lib.last_error() or "hip" in _lib.last_error().lower()
+
+
+def test_error_message_is_thread_local():
+    import threading
+    gemv(M=0)
+    msgs = []
+    t = threading.Thread(target=lambda: msgs.append(_lib.last_error()))
+    t.start()
+    t.join()
+    assert msgs == [""]
+    assert "M=0" in _lib.last_error()
+
+
+def test_python_wrappers_refuse_cpu_tensors():
+    import torch
+    from nativebit_amd import ops
+    with pytest.raises(ValueError, match="GPU"):
+        ops.gemv(torch.zeros(256), torch.zeros(96, dtype=torch.uint8),
+                 torch.zeros(2, 8), 1, 256)
+    with pytest.raises(ValueError, match="GPU"):
+        ops.pack(torch.zeros(8, dtype=torch.uint8), 3)
+
+
+def test_ctypes_types():
+    # the stream argument is a plain pointer in the ABI
+    assert _lib.SIGNATURES["nb_gemv"][1][-1] is ctypes.c_void_p

@@ -1,0 +1,283 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle (run with -m gpu).
+
+Bars (from the north star):
+* unpack / pack / dequant: bit-exact (torch.equal / byte equality);
+* GEMV: ||y - y_ref|| / ||y_ref|| <= 1e-3 against the fp64 brute force for
+  fp32 arithmetic, <= 1e-2 against the reference's bf16 path (weights cast to
+  bf16, inference/eval_ppl.py:149-174) for bf16 activations; golden cases
+  with fp32-exact answers must match exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nativebit_amd import PackedLinear, kernels, ops, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+REL_F32 = 1e-3
+REL_BF16 = 1e-2
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64).reshape(-1)
+    b = np.asarray(b, dtype=np.float64).reshape(-1)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def random_layer(N, K, bits, ne, bs, seed):
+    rng = np.random.default_rng(seed)
+    total = N * K
+    nb = -(-total // bs)
+    idx = rng.integers(0, ne, nb * bs, dtype=np.uint8)
+    cb = (rng.standard_normal((nb, ne)) * 0.02).astype(np.float32)
+    return idx, O.pack(idx, bits), cb
+
+
+# --------------------------------------------------------------------------
+# bit-exact format kernels
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("bits", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("n", [1, 7, 10, 1001, 100_003])
+def test_unpack_pack_bit_exact(dev, bits, n):
+    note(f"unpack/pack bits={bits} n={n}")
+    rng = np.random.default_rng(bits * 7 + n)
+    idx = rng.integers(0, 1 << bits, n, dtype=np.uint8)
+    ref = O.pack(idx, bits)
+    got = ops.pack(torch.from_numpy(idx).to(dev), bits)
+    assert np.array_equal(got.cpu().numpy(), ref)
+    back = ops.unpack(torch.from_numpy(ref).to(dev), n, bits)
+    assert np.array_equal(back.cpu().numpy(), idx)
+
+
+def test_golden_streams_on_gpu(dev, golden):
+    for v in golden["bitstream"]:
+        note(f"golden stream {v['name']}")
+        got = ops.pack(torch.tensor(v["indices"], dtype=torch.uint8, device=dev), v["bits"])
+        assert bytes(got.cpu().numpy()).hex() == v["hex"], v["name"]
+        p = torch.from_numpy(np.frombuffer(bytes.fromhex(v["hex"]), np.uint8).copy()).to(dev)
+        assert ops.unpack(p, len(v["indices"]), v["bits"]).tolist() == v["indices"]
+
+
+@pytest.mark.parametrize("N,K,bits,ne,bs", [
+    (6912, 2560, 3, 8, 128), (2560, 6912, 3, 8, 128), (100, 37, 3, 8, 128),
+    (64, 512, 2, 4, 64), (64, 512, 4, 16, 256), (33, 65, 5, 20, 16), (17, 9, 3, 5, 8),
+])
+def test_dequant_bit_exact(dev, N, K, bits, ne, bs):
+    note(f"dequant N={N} K={K} bits={bits} ne={ne} bs={bs}")
+    idx, p, cb = random_layer(N, K, bits, ne, bs, N + K)
+    ref = O.dequant(idx, cb, bs, N * K)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    w32 = ops.dequant(pt, ct, N * K, bits, bs, torch.float32)
+    assert np.array_equal(w32.cpu().numpy(), ref)
+    w16 = ops.dequant(pt, ct, N * K, bits, bs, torch.bfloat16)
+    assert torch.equal(w16.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
+
+
+def test_reference_gather_equals_dequant(dev):
+    """The reference's own torch unpack+gather (restated) equals nb_dequant."""
+    N, K = 300, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 5)
+    ref = O.torch_dequant(torch.from_numpy(p), torch.from_numpy(cb), N, K, 128, 3)
+    got = ops.dequant(torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N * K, 3, 128)
+    assert torch.equal(got.cpu().reshape(N, K), ref)
+
+
+# --------------------------------------------------------------------------
+# GEMV
+# --------------------------------------------------------------------------
+
+def run_gemv(dev, x, p, cb, N, K, bits, bs, out_dtype=torch.float32):
+    return ops.gemv(x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev),
+                    N, K, bits=bits, block_size=bs, out_dtype=out_dtype)
+
+
+def test_golden_gemv_exact(dev, golden):
+    for g in golden["gemv"]:
+        p = np.frombuffer(bytes.fromhex(g["packed_hex"]), np.uint8).copy()
+        cb = np.array(g["codebook"], np.float32)
+        for xdt in (torch.float32, torch.bfloat16):
+            note(f"golden gemv {g['name']} x={xdt}")
+            x = torch.tensor(g["x"], dtype=torch.float32).to(xdt)
+            y = run_gemv(dev, x, p, cb, g["N"], g["K"], g["bits"], g["block_size"])
+            assert y.cpu().tolist() == g["y"], (g["name"], xdt)
+
+
+@pytest.mark.parametrize("xdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("N,K", [(6912, 2560), (2560, 6912), (2560, 2560), (7680, 2560)])
+def test_gemv_3bit_2p2b_shapes(dev, N, K, xdt):
+    note(f"gemv 3-bit N={N} K={K} x={xdt}")
+    idx, p, cb = random_layer(N, K, 3, 8, 128, N * 3 + K)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(N)).to(xdt)
+    y = run_gemv(dev, x, p, cb, N, K, 3, 128).cpu().numpy()
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+    ref = O.matmul_f64(x.float().numpy(), w)[0]
+    assert rel(y, ref) <= REL_F32, rel(y, ref)
+    if xdt == torch.bfloat16:
+        ref16 = O.torch_packed_linear_bf16(x, torch.from_numpy(p), torch.from_numpy(cb), N, K)
+        assert rel(y, ref16.float().numpy()) <= REL_BF16
+    # the reference kernel's own fp32 order agrees too
+    k1 = O.matvec_3bit_k1(x.float().numpy(), p, cb, N, K)
+    assert rel(y, k1) <= REL_F32
+
+
+@pytest.mark.parametrize("ne,bs", [(4, 64), (4, 128), (4, 256), (8, 64), (8, 128),
+                                   (8, 256), (16, 64), (16, 128), (16, 256)])
+@pytest.mark.parametrize("N,K", [(6912, 2560), (2560, 6912)])
+def test_gemv_bits_block_sweep(dev, ne, bs, N, K):
+    bits = {4: 2, 8: 3, 16: 4}[ne]
+    note(f"gemv sweep ne={ne} bs={bs} N={N} K={K}")
+    idx, p, cb = random_layer(N, K, bits, ne, bs, ne * 1000 + bs + N)
+    x = torch.randn(K, generator=torch.Generator().manual_seed(ne + bs)).to(torch.bfloat16)
+    y = run_gemv(dev, x, p, cb, N, K, bits, bs).cpu().numpy()
+    ref = O.matmul_f64(x.float().numpy(), O.dequant(idx, cb, bs, N * K).reshape(N, K))[0]
+    assert rel(y, ref) <= REL_F32
+
+
+@pytest.mark.parametrize("N,K,bits,ne,bs,M", [
+    (100, 37, 3, 8, 128, 1),     # ragged: blocks straddle rows
+    (61, 300, 3, 8, 16, 3),
+    (257, 1000, 4, 16, 64, 16),
+    (64, 512, 3, 6, 128, 2),     # fewer entries than 2^bits
+    (33, 65, 5, 20, 16, 5),
+    (128, 256, 8, 256, 128, 1),  # unpacked uint8 indices
+    (3000, 2560, 3, 8, 128, 4),
+    (5, 8448, 3, 8, 128, 1),     # K above the fast kernel's limit
+])
+def test_gemv_generic_shapes(dev, N, K, bits, ne, bs, M):
+    note(f"gemv generic N={N} K={K} bits={bits} ne={ne} bs={bs} M={M}")
+    idx, p, cb = random_layer(N, K, bits, ne, bs, N * 13 + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(K))
+    y = run_gemv(dev, x, p, cb, N, K, bits, bs).cpu().numpy()
+    ref = O.matmul_f64(x.numpy(), O.dequant(idx, cb, bs, N * K).reshape(N, K))
+    assert rel(y, ref) <= REL_F32
+
+
+def test_fast_and_generic_agree(dev):
+    """Same problem through both kernels: an x view misaligned to 16 bytes
+    routes the 6912x2560 case to the generic kernel."""
+    N, K = 6912, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 99)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    x_fast = torch.randn(K, generator=torch.Generator().manual_seed(1)).to(dev)
+    x_mis = torch.empty(K + 1, device=dev)
+    x_mis[1:] = x_fast
+    y_fast = ops.gemv(x_fast, pt, ct, N, K)
+    y_slow = ops.gemv(x_mis[1:], pt, ct, N, K)       # 4-byte offset -> generic
+    assert rel(y_slow.cpu(), y_fast.cpu()) <= 1e-5
+
+
+def test_gemv_deterministic(dev):
+    N, K = 6912, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 7)
+    x = torch.randn(K).to(torch.bfloat16)
+    a = run_gemv(dev, x, p, cb, N, K, 3, 128)
+    b = run_gemv(dev, x, p, cb, N, K, 3, 128)
+    assert torch.equal(a, b)
+
+
+def test_gemv_bf16_output(dev):
+    N, K = 2560, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 8)
+    x = torch.randn(K)
+    y32 = run_gemv(dev, x, p, cb, N, K, 3, 128, torch.float32)
+    y16 = run_gemv(dev, x, p, cb, N, K, 3, 128, torch.bfloat16)
+    assert torch.equal(y16.cpu(), y32.cpu().to(torch.bfloat16))
+
+
+def test_gemv_k_zero_writes_zeros(dev):
+    y = torch.full((4,), 7.0, device=dev)
+    ops.gemv(torch.zeros(0, device=dev), torch.zeros(1, dtype=torch.uint8, device=dev),
+             torch.zeros(0, 8, device=dev), 4, 0, out=y.reshape(1, 4))
+    assert y.cpu().tolist() == [0.0] * 4
+
+
+# --------------------------------------------------------------------------
+# operator API (PackedLinear and the function-level mirror)
+# --------------------------------------------------------------------------
+
+def test_packed_linear_api(dev):
+    N, K = 768, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 21)
+    layer = PackedLinear.from_packed(idx.reshape(-1, 128), cb, (N, K), device=dev)
+    assert torch.equal(layer.packed_indices.cpu(), torch.from_numpy(p))
+    assert layer.out_features == N and layer.in_features == K
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+    for shape in [(K,), (1, K), (1, 1, K), (3, K), (2, 5, K), (40, K)]:
+        note(f"PackedLinear x{shape}")
+        x = torch.randn(*shape, generator=torch.Generator().manual_seed(len(shape)))
+        y = layer(x.to(dev))
+        assert y.dtype == torch.float32 and y.shape == (*shape[:-1], N)
+        ref = O.matmul_f64(x.reshape(-1, K).numpy(), w)
+        assert rel(y.cpu().reshape(-1, N), ref) <= REL_F32
+
+
+def test_kernels_mirror(dev):
+    N, K = 512, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 31)
+    x = torch.randn(K)
+    ref = O.matmul_f64(x.numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    for fn in (kernels.dequant_matvec_3bit, kernels.dequant_matvec_3bit_cuda):
+        y = fn(x.to(dev), pt, ct, N, K)
+        assert y.shape == (N,) and rel(y.cpu(), ref) <= REL_F32
+    y8 = kernels.dequant_matvec(x.to(dev), torch.from_numpy(idx.reshape(-1, 128)).to(dev), ct, N, K)
+    assert rel(y8.cpu(), ref) <= REL_F32
+    assert torch.equal(kernels.pack_indices_to_3bit(torch.from_numpy(idx).to(dev)).cpu(),
+                       torch.from_numpy(p))
+
+
+def test_errors_raise_not_fallback(dev):
+    from nativebit_amd import NativeBitError
+    N, K = 64, 256
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 1)
+    layer = PackedLinear.from_packed(idx, cb, (N, K), device=dev)
+    with pytest.raises(ValueError):
+        layer(torch.randn(3, K + 1, device=dev))
+    with pytest.raises(ValueError):
+        layer(torch.randn(3, K))                       # CPU tensor
+    with pytest.raises(NativeBitError):
+        ops.gemv(torch.randn(K, device=dev), layer.packed_indices, layer.codebook, N, K,
+                 bits=9)
+
+
+# --------------------------------------------------------------------------
+# full 2.2B shape: all seven matmul shapes of a layer from the synthetic
+# generator, and size-independent properties over the whole 26-layer model
+# --------------------------------------------------------------------------
+
+def test_synth_layer_all_shapes_vs_f64(dev):
+    for j, (name, N, K) in enumerate(synth.LAYER_SHAPES):
+        note(f"synth layer {name} {N}x{K}")
+        lay = synth.make_layer(N, K, seed=100 + j, device=dev, keep_indices=True)
+        x = synth.make_activation(K, seed=1000 + j, device=dev, dtype=torch.bfloat16)
+        y = ops.gemv(x[0], lay.packed, lay.codebook, N, K).cpu().numpy()
+        idx = lay.indices.cpu().numpy()
+        cb = lay.codebook.cpu().numpy()
+        assert np.array_equal(lay.packed.cpu().numpy(), O.pack(idx, 3))
+        ref = O.matmul_f64(x.float().cpu().numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
+        assert rel(y, ref) <= REL_F32
+
+
+def test_full_model_properties(dev):
+    """26 layers x 7 matmuls at full size: unpack->pack round trip is the
+    identity on every stream, and each GEMV is linear in x."""
+    for layer in range(synth.N_LAYERS):
+        for j, (name, N, K) in enumerate(synth.LAYER_SHAPES):
+            lay = synth.make_layer(N, K, seed=layer * 7 + j, device=dev)
+            idx = ops.unpack(lay.packed, N * K, 3)
+            assert torch.equal(ops.pack(idx, 3), lay.packed)
+            if name in ("q", "down"):
+                note(f"linearity layer {layer} {name}")
+                x1 = synth.make_activation(K, seed=layer, device=dev)[0]
+                x2 = synth.make_activation(K, seed=layer + 500, device=dev)[0]
+                y1 = ops.gemv(x1, lay.packed, lay.codebook, N, K)
+                y2 = ops.gemv(x2, lay.packed, lay.codebook, N, K)
+                y12 = ops.gemv(x1 + x2, lay.packed, lay.codebook, N, K)
+                assert rel(y12.cpu(), (y1 + y2).cpu()) <= 1e-5
