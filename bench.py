@@ -4,16 +4,21 @@
 Workload: 26 layers x 7 packed matmuls (q, k, v, o:
 2560x2560; gate, up: 6912x2560; down: 2560x6912), 3-bit, 8 entries, block
 128, random-init weights quantized as the reference does (per-block quantile
-codebooks, nearest-entry indices), activations bf16 N(0,1), outputs fp32.
-All 182 packed layers (1.29 GB) are resident in HBM, so every step streams
-them from HBM (more than the 256 MB Infinity Cache).
+codebooks, nearest-entry indices), activations bf16 N(0,1) (one independent
+x per matmul, as config 1 defines), outputs fp32.  All 182 packed layers
+(1.29 GB) stay resident in HBM -- more than the 256 MB Infinity Cache -- so
+every step streams them from HBM.
 
-A step is one decode token's worth of GEMVs, launched the way the decode step
-launches them: per layer q|k|v as one GEMV over the three contiguous packed
-matrices (they share x; the reference fuses qkv the same way,
-inference/generate_torch.py:68), o, gate|up as one GEMV (shared x), down --
-4 launches per layer, 104 per step, captured once in a HIP graph and
-replayed.  The JSON line reports total algorithmic bytes / step time.
+A step is one token's 182 GEMVs.  Three launch schedules are timed over the
+same buffers, each captured once in a HIP graph and replayed:
+
+  batched   all 182 GEMVs in one persistent launch (nb_gemv_batched)  <- value
+  per_layer one batched launch per layer (26 launches)
+  decode    the launches a decode step makes: q|k|v, o, gate|up, down per
+            layer (104 nb_gemv launches; q|k|v and gate|up share x)
+
+`value` is the batched schedule: algorithmic bytes per step / HIP-event time
+per replay.  The other two are reported beside it.
 
 Usage: python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -43,73 +48,72 @@ def log(*a):
 
 
 def parse():
-    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p = argparse.ArgumentParser(description=__doc__,
+                                formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--layers", type=int, default=26)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-breakdown", action="store_true")
+    p.add_argument("--schedules", default="batched,per_layer,decode",
+                   help="comma list of schedules to time (batched is the reported value)")
     p.add_argument("--cpu-reps", type=int, default=3)
     return p.parse_args()
 
 
-class Launch:
-    """One nb_gemv call with its buffers and algorithmic byte count."""
+class Mat:
+    """One packed matmul of the model with its own x and y."""
 
-    def __init__(self, name, layers, x, y, packed, cb, N, K):
-        from nativebit_amd import _lib, synth
+    def __init__(self, name, N, K, packed, cb, x, y):
+        from nativebit_amd import synth
         self.name, self.N, self.K = name, N, K
-        self.x, self.y, self.packed, self.cb = x, y, packed, cb
-        self.bytes = sum(synth.layer_bytes(l.out_features, l.in_features, NE, BS, 1, 0, 0)
-                         for l in layers) + K * 2 + N * 4
-        self.args = (x.data_ptr(), _lib.NB_BF16, K, packed.data_ptr(), cb.data_ptr(),
-                     y.data_ptr(), _lib.NB_F32, N, 1, N, K, BITS, NE, BS)
+        self.packed, self.cb, self.x, self.y = packed, cb, x, y
+        self.bytes = synth.layer_bytes(N, K, NE, BS, 1, x_bytes=2, y_bytes=4)
 
 
-def build_step(dev, n_layers):
-    """Generates the 26x7 layers on the GPU and groups them per decode launch."""
+def build_model(dev, n_layers):
+    """182 packed layers generated on the GPU.  q|k|v and gate|up of a layer
+    live in one buffer each (rows never share a block when K % 128 == 0, so
+    the concatenation is byte-identical to one fused packed layer, as the
+    reference fuses qkv, inference/generate_torch.py:68); the individual
+    matrices are views into it."""
     from nativebit_amd import synth
-    launches = []
+    layers = []
     t0 = time.time()
     for l in range(n_layers):
-        mats = {name: synth.make_layer(N, K, NE, BS, seed=l * 7 + j, device=dev)
-                for j, (name, N, K) in enumerate(synth.LAYER_SHAPES)}
-        for gname, members in (("qkv", ("q", "k", "v")), ("o", ("o",)),
-                               ("gateup", ("gate", "up")), ("down", ("down",))):
-            lays = [mats[m] for m in members]
-            K = lays[0].in_features
-            N = sum(m.out_features for m in lays)
-            # rows never share a block (K % BS == 0): the concatenated streams
-            # and codebooks are byte-identical to one (N x K) packed layer.
-            packed = torch.cat([m.packed for m in lays]) if len(lays) > 1 else lays[0].packed
-            cb = torch.cat([m.codebook for m in lays]) if len(lays) > 1 else lays[0].codebook
-            x = synth.make_activation(K, seed=10_000 + l * 7 + len(launches) % 4, device=dev,
-                                      dtype=torch.bfloat16)[0].contiguous()
-            y = torch.empty(N, dtype=torch.float32, device=dev)
-            launches.append(Launch(gname, lays, x, y, packed.contiguous(), cb.contiguous(), N, K))
-        del mats
+        gen = {name: synth.make_layer(N, K, NE, BS, seed=l * 7 + j, device=dev)
+               for j, (name, N, K) in enumerate(synth.LAYER_SHAPES)}
+        mats = {}
+        for group in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            packed = torch.cat([gen[m].packed for m in group]).contiguous()
+            cb = torch.cat([gen[m].codebook for m in group]).contiguous()
+            po = co = 0
+            for m in group:
+                g = gen[m]
+                pn, cn = g.packed.numel(), g.codebook.shape[0]
+                j = [s[0] for s in synth.LAYER_SHAPES].index(m)
+                x = synth.make_activation(g.in_features, seed=100_000 + l * 7 + j, device=dev,
+                                          dtype=torch.bfloat16)[0].contiguous()
+                y = torch.empty(g.out_features, dtype=torch.float32, device=dev)
+                mats[m] = Mat(m, g.out_features, g.in_features, packed[po:po + pn],
+                              cb[co:co + cn], x, y)
+                po += pn
+                co += cn
+            mats["_" + "".join(group)] = (packed, cb)
+        layers.append(mats)
+        del gen
     torch.cuda.synchronize()
     log(f"[bench] generated {n_layers} layers x 7 packed matmuls on {dev} in {time.time()-t0:.1f}s")
-    return launches
+    return layers
 
 
-def run_launches(lib, launches):
-    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    for a in launches:
-        rc = lib.nb_gemv(*a.args, s)
-        if rc:
-            from nativebit_amd import _lib
-            _lib.check(rc)
-
-
-def time_graph(lib, launches, steps, warmup):
-    """Captures one pass over `launches` in a HIP graph; ms per replay."""
-    run_launches(lib, launches)          # eager warm-up (first-call setup)
+def graph_time(run, steps, warmup):
+    """Captures run() once in a HIP graph; returns ms per replay."""
+    run()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        run_launches(lib, launches)
+        run()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -119,32 +123,51 @@ def time_graph(lib, launches, steps, warmup):
         g.replay()
     end.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps, g
+    return start.elapsed_time(end) / steps
 
 
-def check_outputs(launches, n=2):
-    """Spot-checks the first launches' outputs against the fp64 oracle."""
+def decode_launches(layers):
+    """(x, packed, cb, y, N, K) of the 104 decode-step launches."""
+    out = []
+    for mats in layers:
+        qkv_p, qkv_c = mats["_qkv"]
+        gu_p, gu_c = mats["_gateup"]
+        dev = qkv_p.device
+        if "_y_qkv" not in mats:
+            mats["_y_qkv"] = torch.empty(7680, dtype=torch.float32, device=dev)
+            mats["_y_gu"] = torch.empty(13824, dtype=torch.float32, device=dev)
+        out.append((mats["q"].x, qkv_p, qkv_c, mats["_y_qkv"], 7680, 2560))
+        o = mats["o"]
+        out.append((o.x, o.packed, o.cb, o.y, o.N, o.K))
+        out.append((mats["gate"].x, gu_p, gu_c, mats["_y_gu"], 13824, 2560))
+        d = mats["down"]
+        out.append((d.x, d.packed, d.cb, d.y, d.N, d.K))
+    return out
+
+
+def spot_check(mats):
+    """fp64 brute force (bf16-rounded weights, bf16 x) for a few matmuls."""
     import numpy as np
     from oracle import oracle as O
     worst = 0.0
-    for a in launches[:n]:
-        idx = O.unpack(a.packed.cpu().numpy(), a.N * a.K, BITS)
-        w = O.dequant(idx, a.cb.cpu().numpy(), BS, a.N * a.K).reshape(a.N, a.K)
-        ref = O.matmul_f64(a.x.float().cpu().numpy(), w)[0]
-        y = a.y.cpu().numpy()
+    for m in mats:
+        idx = O.unpack(m.packed.cpu().numpy(), m.N * m.K, BITS)
+        w = O.dequant(idx, m.cb.cpu().numpy(), BS, m.N * m.K).reshape(m.N, m.K)
+        w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+        ref = O.matmul_f64(m.x.float().cpu().numpy(), w)[0]
+        y = m.y.cpu().numpy()
         worst = max(worst, float(np.linalg.norm(y - ref) / np.linalg.norm(ref)))
     return worst
 
 
-def cpu_baseline(launches, reps):
+def cpu_baseline(mats, reps):
     """The reference CPU path (unpack + gather + F.linear, restated in
-    oracle.torch_packed_linear_f32) on layer 0's four launches (7 matmuls)."""
+    oracle.torch_packed_linear_f32) on layer 0's 7 matmuls."""
     from oracle import oracle as O
     threads = max(1, min(16, len(os.sched_getaffinity(0))))
     torch.set_num_threads(threads)
-    sample = launches[:4]
-    host = [(a.x.float().cpu(), a.packed.cpu(), a.cb.cpu(), a.N, a.K) for a in sample]
-    nbytes = sum(a.bytes for a in sample)
+    host = [(m.x.float().cpu(), m.packed.cpu(), m.cb.cpu(), m.N, m.K) for m in mats]
+    nbytes = sum(m.bytes for m in mats)
 
     def once():
         for x, p, cb, N, K in host:
@@ -165,10 +188,10 @@ def cpu_baseline(launches, reps):
         pass
     return {
         "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"layer 0 of config 1 (q|k|v, o, gate|up, down = 7 matmuls, {nbytes} B): "
-                   f"torch CPU unpack+gather+F.linear (reference triton_kernel.py:258-275), "
-                   f"x bf16 upcast to fp32, median of {reps} after 1 warm-up, {t*1e3:.1f} ms; "
-                   f"{threads} threads on {cpu_model or platform.processor()}"),
+        "sample": (f"layer 0 of config 1 (q, k, v, o, gate, up, down; {nbytes} B): torch CPU "
+                   f"unpack+gather+F.linear (reference triton_kernel.py:258-275), x bf16 upcast "
+                   f"to fp32, median of {reps} after 1 warm-up = {t*1e3:.1f} ms; {threads} "
+                   f"threads on {cpu_model or platform.processor()}"),
         "seconds_per_sample": round(t, 4),
     }
 
@@ -176,49 +199,67 @@ def cpu_baseline(launches, reps):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build's "
-              "packed GEMV path is single-GPU by design -- run with --gpus 1", file=sys.stderr)
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): the packed GEMV path "
+              "is built and measured on a single MI355X -- run with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a gfx950 GPU", file=sys.stderr)
         sys.exit(1)
-    from nativebit_amd import _lib
+    from nativebit_amd import _lib, ops, synth
     lib = _lib.load()
     dev = torch.device("cuda:0")
     props = torch.cuda.get_device_properties(dev)
-    log(f"[bench] {torch.cuda.get_device_name(dev)} {props.gcnArchName} CUs={props.multi_processor_count}")
+    log(f"[bench] {torch.cuda.get_device_name(dev)} {props.gcnArchName} "
+        f"CUs={props.multi_processor_count}")
 
-    launches = build_step(dev, args.layers)
-    step_bytes = sum(a.bytes for a in launches)
-    ms, _ = time_graph(lib, launches, args.steps, args.warmup)
-    gbs = step_bytes / (ms * 1e-3) / 1e9
-    err = check_outputs(launches)
-    log(f"[bench] decode schedule: {len(launches)} launches/step, {step_bytes} B/step, "
-        f"{ms*1e3:.1f} us/step, {gbs:.1f} GB/s ({100*gbs/HBM_PEAK_GBS:.1f}% of 8 TB/s), "
+    layers = build_model(dev, args.layers)
+    all_mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
+    step_bytes = sum(m.bytes for m in all_mats)
+    wanted = args.schedules.split(",")
+    results = {}
+
+    batch = ops.GemvBatch([(m.x, m.packed, m.cb, m.y, m.N, m.K) for m in all_mats])
+    ms = graph_time(batch.run, args.steps, args.warmup)
+    err = spot_check(all_mats[:7])
+    results["batched"] = {"launches": 1, "us_per_step": round(ms * 1e3, 2),
+                          "GB_s": round(step_bytes / ms / 1e6, 1)}
+    log(f"[bench] batched  : 1 launch/step, {step_bytes} B, {ms*1e3:.1f} us/step, "
+        f"{step_bytes/ms/1e6:.1f} GB/s ({step_bytes/ms/1e6/HBM_PEAK_GBS*100:.1f}% of 8 TB/s), "
         f"spot-check rel err {err:.2e}")
 
-    extra = {}
-    if not args.no_breakdown:
-        breakdown = {}
-        for gname in ("qkv", "o", "gateup", "down"):
-            sub = [a for a in launches if a.name == gname]
-            sms, _ = time_graph(lib, sub, max(10, args.steps // 2), 3)
-            sb = sum(a.bytes for a in sub)
-            breakdown[gname] = {"N": sub[0].N, "K": sub[0].K, "launches": len(sub),
-                                "us_per_launch": round(sms * 1e3 / len(sub), 3),
-                                "GB_s": round(sb / (sms * 1e-3) / 1e9, 1)}
-            log(f"[bench]   {gname:6s} {sub[0].N}x{sub[0].K}: {sms*1e3/len(sub):.2f} us/launch, "
-                f"{breakdown[gname]['GB_s']:.1f} GB/s")
-        extra["breakdown"] = breakdown
-        # eager (no graph) for reference: includes host launch overhead
-        run_launches(lib, launches)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(5):
-            run_launches(lib, launches)
-        torch.cuda.synchronize()
-        extra["eager_us_per_step"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+    if "per_layer" in wanted:
+        per = [ops.GemvBatch([(mats[n].x, mats[n].packed, mats[n].cb, mats[n].y,
+                               mats[n].N, mats[n].K) for n in ("q", "k", "v", "o", "gate", "up",
+                                                               "down")]) for mats in layers]
 
+        def run_per():
+            for b in per:
+                b.run()
+        pms = graph_time(run_per, max(10, args.steps // 2), args.warmup)
+        results["per_layer"] = {"launches": len(per), "us_per_step": round(pms * 1e3, 2),
+                                "GB_s": round(step_bytes / pms / 1e6, 1)}
+        log(f"[bench] per_layer: {len(per)} launches/step, {pms*1e3:.1f} us/step, "
+            f"{step_bytes/pms/1e6:.1f} GB/s")
+
+    if "decode" in wanted:
+        dl = decode_launches(layers)
+        dec_bytes = sum(synth.layer_bytes(N, K, NE, BS, 1, 2, 4) for (_, _, _, _, N, K) in dl)
+        args_c = [(x.data_ptr(), _lib.NB_BF16, K, p.data_ptr(), c.data_ptr(), y.data_ptr(),
+                   _lib.NB_F32, N, 1, N, K, BITS, NE, BS) for (x, p, c, y, N, K) in dl]
+
+        def run_dec():
+            s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            for a in args_c:
+                rc = lib.nb_gemv(*a, s)
+                if rc:
+                    _lib.check(rc)
+        dms = graph_time(run_dec, max(10, args.steps // 2), args.warmup)
+        results["decode"] = {"launches": len(dl), "us_per_step": round(dms * 1e3, 2),
+                             "GB_s": round(dec_bytes / dms / 1e6, 1), "bytes_per_step": dec_bytes}
+        log(f"[bench] decode   : {len(dl)} launches/step, {dms*1e3:.1f} us/step, "
+            f"{dec_bytes/dms/1e6:.1f} GB/s")
+
+    gbs = step_bytes / ms / 1e6
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -230,16 +271,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": ("config1: 2.2B-shape decode-step GEMVs, 26 layers x (q,k,v,o 2560x2560; "
+            "workload": ("config1: 2.2B-shape GEMVs of one token, 26 layers x (q,k,v,o 2560x2560; "
                          "gate,up 6912x2560; down 2560x6912), 3-bit NE 8 BS 128, batch 1, "
-                         "x bf16 N(0,1), y fp32, weights fp32 codebook values"),
-            "schedule": "per layer: qkv, o, gate|up, down (104 launches/step, HIP graph)",
+                         "x bf16 N(0,1) per matmul, y fp32, bf16 weights, fp32 accumulation"),
+            "schedule": "batched: all 182 GEMVs in one persistent launch (HIP graph replay)",
             "layers": args.layers,
             "bytes_per_step": step_bytes,
-            "tokens_per_s_gemv_only": round(1e3 / ms, 1),
+            "gemv_steps_per_s": round(1e3 / ms, 1),
             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         },
         "roofline": {
@@ -249,16 +290,18 @@ def main():
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
-            "kernel": "gemv_fast_kernel<3,128,bf16x>",
-            "method": "algorithmic bytes of all launches in the timed region / HIP-event time "
-                      "of the graph replays on the launch stream",
+            "kernel": "gemv_stream_kernel",
+            "method": ("algorithmic bytes per launch (0.625 B/weight + x + y) / HIP-event time "
+                       "per graph replay of the single launch, on the launch stream"),
         },
+        "schedules": results,
         "parity": {"spot_check_rel_err_vs_f64": err},
     }
-    result.update(extra)
     if not args.no_cpu_baseline:
         log("[bench] timing CPU baseline ...")
-        result["cpu_baseline"] = cpu_baseline(launches, args.cpu_reps)
+        result["cpu_baseline"] = cpu_baseline([layers[0][n] for n in
+                                               ("q", "k", "v", "o", "gate", "up", "down")],
+                                              args.cpu_reps)
         log(f"[bench] cpu baseline {result['cpu_baseline']['value']} GB/s "
             f"({result['cpu_baseline']['cores']} threads)")
     print(json.dumps(result), flush=True)

@@ -26,9 +26,11 @@
  *     memory and never synchronizes.  Work is enqueued on `stream` (a
  *     hipStream_t; NULL = the default stream) and is graph-capturable.
  *   - Element types are passed as nb_dtype codes; activations x and outputs
- *     y may be NB_F32 or NB_BF16.  Arithmetic: weights are the exact fp32
- *     codebook values, x is widened to fp32, products and sums are fp32
- *     (nb_gemm_prefill: weights and x rounded to bf16, fp32 accumulation).
+ *     y may be NB_F32 or NB_BF16.  Arithmetic: with NB_F32 activations the
+ *     weights are the exact fp32 codebook values; with NB_BF16 activations
+ *     they are the codebook values rounded to bf16 (round to nearest even),
+ *     the reference's bf16 path (inference/eval_ppl.py:149-174).  Products
+ *     are exact in fp32 and sums are fp32.
  */
 #ifndef NATIVEBIT_AMD_H
 #define NATIVEBIT_AMD_H
@@ -121,6 +123,46 @@ int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits,
 int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out,
                int w_dtype, int64_t total, int64_t num_blocks, int bits,
                int n_entries, int block_size, void* stream);
+
+/*
+ * Batched GEMV: many independent 3-bit / 8-entry / block-128 GEMVs
+ * (bf16 x of one row, M = 1) streamed by one persistent launch.
+ *
+ * No counterpart in the reference, whose operator runs one layer per call
+ * (inference/triton_kernel.py:240-257).  It serves callers that hold several
+ * packed layers with their activations ready at once -- the projections of
+ * one decode step that share no dependency, or a sweep over all layers -- so
+ * that the per-launch cost (about 1.6 us on MI355X) and the ramp of each
+ * small launch are paid once.  Each item is exactly nb_gemv(x, NB_BF16, ...,
+ * M = 1) of that item.
+ *
+ * Usage: nb_gemv_batch_plan() validates the items and writes a device-ready
+ * table into caller host memory; the caller copies that table to device
+ * memory once and passes it to nb_gemv_batched() (with the same items) on
+ * every call.  x, packed and codebook of every item must be 16-byte aligned
+ * and K % 128 == 0, K <= 8192.
+ */
+typedef struct nb_batch_item {
+    const void* x;          /* K bf16 activations                          */
+    const uint8_t* packed;  /* 3-bit stream of N*K indices                 */
+    const float* codebook;  /* (N*K/128) x 8 fp32                          */
+    void* y;                /* N outputs of y_dtype                        */
+    int32_t N;
+    int32_t K;
+} nb_batch_item;
+
+/* Bytes of the device table for `count` items. */
+int64_t nb_gemv_batch_table_bytes(int count);
+
+/* Validates items and writes the table (nb_gemv_batch_table_bytes(count)
+ * bytes) into table_host. */
+int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
+                       int64_t table_bytes);
+
+/* Runs the batch: table_dev is the device copy of nb_gemv_batch_plan's
+ * output for the same items. */
+int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count,
+                    int y_dtype, void* stream);
 
 #ifdef __cplusplus
 }

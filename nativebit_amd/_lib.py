@@ -47,7 +47,17 @@ SIGNATURES = {
     "nb_unpack": (_I, [_P, _P, _L, _I, _P]),
     "nb_pack": (_I, [_P, _P, _L, _I, _P]),
     "nb_dequant": (_I, [_P, _P, _P, _I, _L, _L, _I, _I, _I, _P]),
+    "nb_gemv_batch_table_bytes": (_L, [_I]),
+    "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
+    "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),
 }
+
+
+class BatchItem(ctypes.Structure):
+    """struct nb_batch_item (include/nativebit_amd.h)."""
+    _fields_ = [("x", ctypes.c_void_p), ("packed", ctypes.c_void_p),
+                ("codebook", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
 
 
 class NativeBitError(RuntimeError):

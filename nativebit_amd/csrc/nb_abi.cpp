@@ -20,6 +20,7 @@ thread_local char g_last_error[512] = "";
 
 constexpr int kMaxDevices = 64;
 int g_cu_count[kMaxDevices];
+int g_lds_bytes[kMaxDevices];
 int g_device_ok[kMaxDevices];  // 0 unknown, 1 gfx950, -1 unusable
 std::mutex g_dev_mutex;
 
@@ -56,6 +57,7 @@ int ensure_device() {
         } else {
             g_device_ok[dev] = 1;
             g_cu_count[dev] = prop.multiProcessorCount;
+            g_lds_bytes[dev] = (int)prop.sharedMemPerBlock;
         }
     }
     if (g_device_ok[dev] != 1) {
@@ -95,6 +97,13 @@ int device_cu_count() {
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
     std::lock_guard<std::mutex> lock(g_dev_mutex);
     return g_cu_count[dev] > 0 ? g_cu_count[dev] : 256;
+}
+
+int device_lds_bytes() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 64 * 1024;
+    std::lock_guard<std::mutex> lock(g_dev_mutex);
+    return g_lds_bytes[dev] > 0 ? g_lds_bytes[dev] : 64 * 1024;
 }
 
 }  // namespace nb
@@ -190,6 +199,115 @@ int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out, int w_
     if (st) return st;
     return launch_dequant(packed, codebook, w_out, w_dtype, total, num_blocks, bits, n_entries,
                           block_size, static_cast<hipStream_t>(stream));
+}
+
+int64_t nb_gemv_batch_table_bytes(int count) {
+    return count > 0 ? (int64_t)count * (int64_t)sizeof(StreamProblem) : 0;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Shared validation of batch items; fills total tiles and the largest K.
+int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* total_steps,
+                int* max_k) {
+    if (count < 0) return fail(NB_EINVAL, "%s: count=%d < 0", fn, count);
+    if (count > 0 && !items) return fail(NB_EINVAL, "%s: items is NULL", fn);
+    int64_t steps = 0;
+    int mk = 0;
+    for (int i = 0; i < count; ++i) {
+        const nb_batch_item& it = items[i];
+        if (it.N < 0 || it.K < 0) return fail(NB_EINVAL, "%s: item %d has a negative shape", fn, i);
+        if (it.N == 0) continue;
+        if (it.K == 0 || it.K % 128 != 0 || it.K > 8192) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d K=%d (needs K %% 128 == 0, 0 < K <= 8192)",
+                        fn, i, it.K);
+        }
+        if (!it.x || !it.packed || !it.codebook || !it.y) {
+            return fail(NB_EINVAL, "%s: item %d has a NULL pointer", fn, i);
+        }
+        if (!aligned(it.x, 16) || !aligned(it.packed, 16) || !aligned(it.codebook, 16)) {
+            return fail(NB_EALIGN, "%s: item %d x/packed/codebook not 16-byte aligned", fn, i);
+        }
+        if (!aligned(it.y, 2)) return fail(NB_EALIGN, "%s: item %d y not 2-byte aligned", fn, i);
+        steps += (int64_t)((it.N + 15) / 16) * ((it.K / 128 + 3) / 4);
+        if (it.K > mk) mk = it.K;
+    }
+    if (steps > INT32_MAX) return fail(NB_EUNSUPPORTED, "%s: %lld steps exceed int32", fn, (long long)steps);
+    *total_steps = steps;
+    *max_k = mk;
+    return NB_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
+                       int64_t table_bytes) {
+    const char* fn = "nb_gemv_batch_plan";
+    int64_t steps = 0;
+    int mk = 0;
+    int st = check_batch(items, count, fn, &steps, &mk);
+    if (st) return st;
+    if (table_bytes < nb_gemv_batch_table_bytes(count)) {
+        return fail(NB_EINVAL, "%s: table of %lld bytes, %lld needed", fn, (long long)table_bytes,
+                    (long long)nb_gemv_batch_table_bytes(count));
+    }
+    if (count > 0 && !table_host) return fail(NB_EINVAL, "%s: table_host is NULL", fn);
+    // Items with N == 0 are left out; the table holds the others in order and
+    // the unused tail of the table is zeroed.
+    StreamProblem* t = static_cast<StreamProblem*>(table_host);
+    memset(table_host, 0, (size_t)nb_gemv_batch_table_bytes(count));
+    int32_t begin = 0, step_begin = 0;
+    int n = 0;
+    for (int i = 0; i < count; ++i) {
+        const nb_batch_item& it = items[i];
+        if (it.N == 0) continue;
+        StreamProblem p;
+        memset(&p, 0, sizeof(p));
+        p.x = static_cast<const uint16_t*>(it.x);
+        p.packed = it.packed;
+        p.codebook = it.codebook;
+        p.y = it.y;
+        p.N = it.N;
+        p.K = it.K;
+        p.bpr = it.K / 128;
+        p.nsteps = (p.bpr + 3) / 4;
+        p.tiles = (it.N + 15) / 16;
+        p.tile_begin = begin;
+        p.step_begin = step_begin;
+        begin += p.tiles;
+        step_begin += p.tiles * p.nsteps;
+        t[n++] = p;
+    }
+    return NB_OK;
+}
+
+int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count, int y_dtype,
+                    void* stream) {
+    const char* fn = "nb_gemv_batched";
+    int64_t steps = 0;
+    int mk = 0;
+    int st = check_batch(items, count, fn, &steps, &mk);
+    if (st) return st;
+    if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
+    if (steps == 0) return NB_OK;
+    if (!table_dev) return fail(NB_EINVAL, "%s: table_dev is NULL", fn);
+    if (!aligned(table_dev, 8)) return fail(NB_EALIGN, "%s: table_dev not 8-byte aligned", fn);
+    int nprob = 0;
+    for (int i = 0; i < count; ++i) {
+        if (items[i].N == 0) continue;
+        ++nprob;
+        if (y_dtype == NB_F32 && !aligned(items[i].y, 4)) {
+            return fail(NB_EALIGN, "%s: item %d y not 4-byte aligned", fn, i);
+        }
+    }
+    st = ensure_device();
+    if (st) return st;
+    return launch_gemv_stream(static_cast<const StreamProblem*>(table_dev), nprob, (int)steps, mk,
+                              y_dtype, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -22,8 +22,14 @@
 //   stream.  Used for ragged shapes and as an independent statement of the
 //   arithmetic.
 //
-// Arithmetic for both: the exact fp32 codebook value times x widened to fp32,
-// fp32 FMA accumulation; y is stored as fp32 or rounded to bf16 (RNE).
+// Arithmetic for both: with fp32 x the exact fp32 codebook value, with bf16 x
+// the codebook value rounded to bf16 (the reference's bf16 semantics,
+// inference/eval_ppl.py:166; nb_gemv_mfma.hip computes the same), times x
+// widened to fp32, fp32 FMA accumulation; y is stored as fp32 or rounded to
+// bf16 (RNE).
+//
+// The bf16-activation 3-bit / 8-entry / block-128 case is taken by the MFMA
+// kernel in nb_gemv_mfma.hip before either kernel here is considered.
 #include "nb_device.h"
 #include "nb_internal.h"
 
@@ -70,7 +76,8 @@ __global__ __launch_bounds__(kThreads) void gemv_generic_kernel(GemvArgs a) {
             const int64_t flat = (int64_t)n * a.K + k;
             uint32_t e = read_field(a.packed, a.packed_bytes, flat, a.bits);
             e = e < last ? e : last;
-            const float w = a.codebook[(flat / a.block_size) * a.n_entries + e];
+            float w = a.codebook[(flat / a.block_size) * a.n_entries + e];
+            if (a.x_dtype == NB_BF16) w = round_bf16(w);
 #pragma unroll
             for (int m = 0; m < kMaxM; ++m) {
                 if (m < a.M) acc[m] = fmaf(w, load_x(a.x, a.x_dtype, m * a.ldx + k), acc[m]);
@@ -196,7 +203,40 @@ __device__ __forceinline__ float slice_dot(const uint32_t (&d)[BITS], uint32_t b
     return a0 + a1;
 }
 
-template <int BITS, int BS, bool kXBF16, int R>
+// Pipeline depth of the streaming kernel (row-sets whose loads are in flight
+// per lane) and resident workgroups per CU it is launched with.
+#ifndef NB_GEMV_DEPTH
+#define NB_GEMV_DEPTH 4
+#endif
+#ifndef NB_GEMV_WG_PER_CU
+#define NB_GEMV_WG_PER_CU 4
+#endif
+
+// Row-set `set` of the stream: this lane's BITS dwords and EPL codebook
+// entries (loads only; nothing waits here).
+template <int BITS, int BS, int EPL>
+__device__ __forceinline__ void issue_set(const uint32_t* __restrict__ packed,
+                                          const float* __restrict__ cb, int row,
+                                          int S, int s, int bpr, int q,
+                                          uint32_t (&d)[BITS], float (&cv)[EPL]) {
+    constexpr int NE = 1 << BITS;
+    constexpr int SPB = BS / 32;
+    const uint32_t* pk = packed + ((int64_t)row * S + s) * BITS;
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) d[w] = stream_load(pk + w);
+    const float* c = cb + ((int64_t)row * bpr + s / SPB) * NE + q * EPL;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        if (q * EPL + e < NE) cv[e] = stream_load(c + e);
+    }
+}
+
+// Each workgroup streams a contiguous range of row-sets.  Lane registers
+// hold a ring of D row-sets: the loads of set i+D are issued right after set
+// i has been consumed, so every lane keeps D sets of HBM requests in flight
+// while it computes.  The weight loads of the first D sets are issued before
+// the activations are fetched, so the two latencies overlap.
+template <int BITS, int BS, bool kXBF16, int D>
 __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ packed,
     const float* __restrict__ cb, void* __restrict__ y, int y_dtype, int N,
@@ -205,8 +245,8 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
     constexpr int SPB = BS / 32;                  // slices (lanes) per block
     constexpr int NSLOT = kThreads / SPB;         // blocks per row-set
     constexpr int EPL = (NE + SPB - 1) / SPB;     // entries staged per lane
-    __shared__ float s_cb[R][NSLOT * NE];
-    __shared__ float s_red[R][kThreads / 8];
+    __shared__ float s_cb[NSLOT * NE];
+    __shared__ float s_red[2][kThreads / 8];
 
     const int t = threadIdx.x;
     const int S = K >> 5;           // slices per row
@@ -217,117 +257,104 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
     const int slot = t / SPB;
     const int q = t - slot * SPB;
 
-    float xr[32];
-    if (lane_on) {
-        load_x_slice<kXBF16>(x, s, xr);
-    } else {
+    // contiguous, balanced range of row-sets for this workgroup
+    const int per = n_sets / gridDim.x;
+    const int rem = n_sets - per * gridDim.x;
+    const int b = blockIdx.x;
+    const int set_begin = b * per + (b < rem ? b : rem);
+    const int count = per + (b < rem ? 1 : 0);
+
+    // Loads are never predicated (a predicated load makes the compiler copy
+    // its result right away, i.e. wait for it): lanes past the last row or
+    // set load a clamped, already-cached address and their sums are dropped.
+    const int last_set = set_begin + count - 1;
+    auto clamp_row = [&](int set) {
+        const int r = (set < last_set ? set : last_set) * P + row_sub;
+        return r < N ? r : N - 1;
+    };
+    uint32_t d[D][BITS];
+    float cv[D][EPL];
 #pragma unroll
-        for (int j = 0; j < 32; ++j) xr[j] = 0.f;
+    for (int st = 0; st < D; ++st) {
+        issue_set<BITS, BS, EPL>(packed, cb, clamp_row(set_begin + st), S, s, bpr, q,
+                                 d[st], cv[st]);
     }
 
-    for (int set0 = blockIdx.x * R; set0 < n_sets; set0 += gridDim.x * R) {
-        uint32_t d[R][BITS];
-        float cv[R][EPL];
-        bool valid[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int row = (set0 + r) * P + row_sub;
-            valid[r] = lane_on && (set0 + r) < n_sets && row < N;
-            if (valid[r]) {
-                const uint32_t* pk = packed + ((int64_t)row * S + s) * BITS;
-#pragma unroll
-                for (int w = 0; w < BITS; ++w) d[r][w] = __builtin_nontemporal_load(pk + w);
-                const float* c = cb + ((int64_t)row * bpr + s / SPB) * NE + q * EPL;
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    if (q * EPL + e < NE) cv[r][e] = __builtin_nontemporal_load(c + e);
-                }
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            if (valid[r]) {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    if (q * EPL + e < NE) s_cb[r][slot * NE + q * EPL + e] = cv[r][e];
-                }
-            }
-        }
-        // The SPB lanes that share a slot are consecutive threads of one
-        // wave and a wave's LDS operations complete in issue order, so the
-        // table written above is visible to the reads below without a
-        // workgroup barrier.
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float xr[32];
+    load_x_slice<kXBF16>(x, s, xr);
 
-        float acc[R];
+    for (int base = 0; base < count; base += D) {
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] = 0.f;
-            if (valid[r]) {
-                acc[r] = slice_dot<BITS>(d[r], (uint32_t)(slot * NE * 4),
-                                         reinterpret_cast<const char*>(&s_cb[r][0]), xr);
+        for (int st = 0; st < D; ++st) {
+            const int i = base + st;
+            if (i < count) {  // uniform over the workgroup
+                const int set = set_begin + i;
+                const bool valid = lane_on && set * P + row_sub < N;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    if (q * EPL + e < NE) {
+                        s_cb[slot * NE + q * EPL + e] = kXBF16 ? round_bf16(cv[st][e]) : cv[st][e];
+                    }
+                }
+                // The SPB lanes sharing a slot are consecutive lanes of one
+                // wave and a wave's LDS operations complete in issue order:
+                // the table is visible below without a barrier, and the next
+                // set's write comes after these reads.
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                float acc = slice_dot<BITS>(d[st], (uint32_t)(slot * NE * 4),
+                                            reinterpret_cast<const char*>(s_cb), xr);
+                acc = valid ? acc : 0.f;
+                issue_set<BITS, BS, EPL>(packed, cb, clamp_row(set + D), S, s, bpr, q,
+                                         d[st], cv[st]);
+                // 8 consecutive lanes always belong to one row (S % 8 == 0).
+                acc += __shfl_xor(acc, 1, 8);
+                acc += __shfl_xor(acc, 2, 8);
+                acc += __shfl_xor(acc, 4, 8);
+                float* red = s_red[i & 1];
+                if ((t & 7) == 0) red[t >> 3] = acc;
+                // one barrier per set: s_red is double buffered, so the next
+                // set writes the other half while this one is summed.
+                __syncthreads();
+                if (t < P) {
+                    const int orow = set * P + t;
+                    if (orow < N) {
+                        const int ng = S >> 3;
+                        float sum = 0.f;
+                        for (int g = t * ng; g < (t + 1) * ng; ++g) sum += red[g];
+                        store_y(y, y_dtype, orow, sum);
+                    }
+                }
             }
         }
-        // 8 consecutive lanes always belong to one row (S % 8 == 0).
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            acc[r] += __shfl_xor(acc[r], 1, 8);
-            acc[r] += __shfl_xor(acc[r], 2, 8);
-            acc[r] += __shfl_xor(acc[r], 4, 8);
-        }
-        if ((t & 7) == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) s_red[r][t >> 3] = acc[r];
-        }
-        __syncthreads();
-        if (t < R * P) {
-            const int r = t / P;
-            const int p = t - r * P;
-            const int set = set0 + r;
-            const int row = set * P + p;
-            if (set < n_sets && row < N) {
-                const int ng = S >> 3;
-                float sum = 0.f;
-                for (int g = p * ng; g < (p + 1) * ng; ++g) sum += s_red[r][g];
-                store_y(y, y_dtype, row, sum);
-            }
-        }
-        __syncthreads();
     }
 }
 
 typedef void (*FastFn)(const void*, const uint32_t*, const float*, void*, int,
                        int, int, int, int);
 
-template <int BITS, int BS, bool XB>
-FastFn pick_r(int r) {
-    if (r == 4) return gemv_fast_kernel<BITS, BS, XB, 4>;
-    if (r == 2) return gemv_fast_kernel<BITS, BS, XB, 2>;
-    return gemv_fast_kernel<BITS, BS, XB, 1>;
-}
-
 template <int BITS, int BS>
-FastFn pick_x(bool xb, int r) {
-    return xb ? pick_r<BITS, BS, true>(r) : pick_r<BITS, BS, false>(r);
+FastFn pick_x(bool xb) {
+    return xb ? gemv_fast_kernel<BITS, BS, true, NB_GEMV_DEPTH>
+              : gemv_fast_kernel<BITS, BS, false, NB_GEMV_DEPTH>;
 }
 
 template <int BITS>
-FastFn pick_bs(int bs, bool xb, int r) {
+FastFn pick_bs(int bs, bool xb) {
     switch (bs) {
-        case 64: return pick_x<BITS, 64>(xb, r);
-        case 128: return pick_x<BITS, 128>(xb, r);
-        case 256: return pick_x<BITS, 256>(xb, r);
+        case 64: return pick_x<BITS, 64>(xb);
+        case 128: return pick_x<BITS, 128>(xb);
+        case 256: return pick_x<BITS, 256>(xb);
     }
     return nullptr;
 }
 
-FastFn pick_fast(int bits, int bs, bool xb, int r) {
+FastFn pick_fast(int bits, int bs, bool xb) {
     switch (bits) {
-        case 2: return pick_bs<2>(bs, xb, r);
-        case 3: return pick_bs<3>(bs, xb, r);
-        case 4: return pick_bs<4>(bs, xb, r);
+        case 2: return pick_bs<2>(bs, xb);
+        case 3: return pick_bs<3>(bs, xb);
+        case 4: return pick_bs<4>(bs, xb);
     }
     return nullptr;
 }
@@ -355,16 +382,15 @@ int launch_gemv(const GemvArgs& a, hipStream_t stream) {
                            a.y, a.y_dtype, a.M, a.N, a.ldy);
         return check_launch("nb_gemv (K == 0)");
     }
+    const int st = launch_gemv_mfma(a, stream);
+    if (st != 1) return st;
     if (fast_eligible(a)) {
         const int S = a.K / 32;
         const int P = kThreads / S;
         const int n_sets = (a.N + P - 1) / P;
-        int r = 1;
-        if (n_sets >= 4 * 2 * cus) r = 4;
-        else if (n_sets >= 2 * 2 * cus) r = 2;
-        int64_t grid = (n_sets + r - 1) / r;
-        if (grid > (int64_t)cus * 8) grid = (int64_t)cus * 8;
-        FastFn fn = pick_fast(a.bits, a.block_size, a.x_dtype == NB_BF16, r);
+        int64_t grid = (int64_t)cus * NB_GEMV_WG_PER_CU;
+        if (grid > n_sets) grid = n_sets;
+        FastFn fn = pick_fast(a.bits, a.block_size, a.x_dtype == NB_BF16);
         hipLaunchKernelGGL(fn, dim3((int)grid), dim3(kThreads), 0, stream, a.x,
                            reinterpret_cast<const uint32_t*>(a.packed), a.codebook,
                            a.y, a.y_dtype, a.N, a.K, P, n_sets);

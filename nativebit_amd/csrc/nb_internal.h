@@ -18,6 +18,8 @@ int check_launch(const char* what);
 
 // Multiprocessor count of the current device (cached per device).
 int device_cu_count();
+// Shared memory (LDS) bytes one workgroup may use on the current device.
+int device_lds_bytes();
 
 // Packed stream length, mirroring nb_packed_nbytes.
 inline int64_t packed_nbytes(int64_t count, int bits) {
@@ -39,8 +41,30 @@ struct GemvArgs {
     int M, N, K, bits, n_entries, block_size;
 };
 
+// One GEMV of a batch as the streaming kernel reads it (device table entry,
+// written on the host by nb_gemv_batch_plan).
+struct StreamProblem {
+    const uint16_t* x;        // K bf16 activations
+    const uint8_t* packed;    // 3-bit stream
+    const float* codebook;    // (N*K/128) x 8
+    void* y;                  // N outputs
+    int32_t N, K;
+    int32_t bpr;              // 128-weight blocks per row
+    int32_t nsteps;           // 512-column steps per row (ceil(bpr / 4))
+    int32_t tiles;            // 16-row tiles
+    int32_t tile_begin;       // first tile's index in the batch
+    int32_t step_begin;       // steps of all earlier problems (tiles * nsteps)
+    int32_t pad;
+};
+
+int launch_gemv_stream(const StreamProblem* dev_probs, int nprob, int total_steps,
+                       int max_k, int y_dtype, hipStream_t stream);
+
 // Kernel launchers (arguments already validated by nb_abi.cpp).
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
+// The bf16-activation MFMA GEMV; returns 1 (launching nothing) when the
+// problem is outside its 3-bit / 8-entry / block-128 / aligned domain.
+int launch_gemv_mfma(const GemvArgs& a, hipStream_t stream);
 int launch_unpack(const uint8_t* packed, uint8_t* out, int64_t count, int bits,
                   hipStream_t stream);
 int launch_pack(const uint8_t* idx, uint8_t* out, int64_t count, int bits,

@@ -90,6 +90,53 @@ def gemv(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
     return out.reshape(N) if squeeze else out
 
 
+class GemvBatch:
+    """Many independent 3-bit GEMVs (bf16 x, M = 1) in one persistent launch.
+
+    items: sequence of (x, packed, codebook, y, N, K) with x a (K,) bf16
+    tensor, packed/codebook a 3-bit / 8-entry / block-128 layer and y an (N,)
+    float32 or bfloat16 output.  The device table is built once here; each
+    run() enqueues one launch on torch's current stream (graph-capturable).
+    The tensors are referenced by pointer: keep them alive and in place.
+    """
+
+    def __init__(self, items):
+        self.items = list(items)
+        n = len(self.items)
+        self._arr = (_lib.BatchItem * max(n, 1))()
+        y_dt = None
+        for i, (x, packed, cb, y, N, K) in enumerate(self.items):
+            for name, t in (("x", x), ("packed", packed), ("codebook", cb), ("y", y)):
+                _require_cuda(name, t)
+            if x.dtype != torch.bfloat16 or x.numel() != K or not x.is_contiguous():
+                raise TypeError(f"item {i}: x must be a contiguous ({K},) bfloat16 tensor")
+            if packed.dtype != torch.uint8 or cb.dtype != torch.float32:
+                raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
+            if cb.shape != (N * K // 128, 8) or packed.numel() < packed_nbytes(N * K, 3):
+                raise ValueError(f"item {i}: not a 3-bit / 8-entry / block-128 {N}x{K} layer")
+            if y.numel() != N or y.dtype not in _DT or not y.is_contiguous():
+                raise ValueError(f"item {i}: y must be a contiguous ({N},) float32/bfloat16 tensor")
+            if y_dt is None:
+                y_dt = y.dtype
+            elif y.dtype != y_dt:
+                raise TypeError("all outputs of a batch share one dtype")
+            self._arr[i] = _lib.BatchItem(x.data_ptr(), packed.data_ptr(), cb.data_ptr(),
+                                          y.data_ptr(), int(N), int(K))
+        self.y_dtype = y_dt or torch.float32
+        lib = _lib.load()
+        nbytes = int(lib.nb_gemv_batch_table_bytes(n))
+        host = torch.zeros(max(nbytes, 8), dtype=torch.uint8)
+        _lib.check(lib.nb_gemv_batch_plan(self._arr, n, host.data_ptr(), nbytes))
+        dev = self.items[0][0].device if n else torch.device("cuda")
+        self.table = host.to(dev)
+        self.count = n
+
+    def run(self):
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.table.device).cuda_stream)
+        _lib.check(_lib.load().nb_gemv_batched(self._arr, self.table.data_ptr(), self.count,
+                                               _DT[self.y_dtype], stream))
+
+
 def unpack(packed: torch.Tensor, count: int, bits: int) -> torch.Tensor:
     """uint8 indices from an LSB-first stream (device)."""
     _require_cuda("packed", packed)

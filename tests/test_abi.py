@@ -132,3 +132,28 @@ def test_python_wrappers_refuse_cpu_tensors():
 def test_ctypes_types():
     # the stream argument is a plain pointer in the ABI
     assert _lib.SIGNATURES["nb_gemv"][1][-1] is ctypes.c_void_p
+
+
+def test_batch_validation():
+    lib = _lib.load()
+    Item = _lib.BatchItem
+    good = Item(FAKE, FAKE, FAKE, FAKE, 32, 256)
+    arr = (Item * 2)(good, good)
+    nbytes = lib.nb_gemv_batch_table_bytes(2)
+    assert nbytes > 0 and lib.nb_gemv_batch_table_bytes(0) == 0
+    buf = ctypes.create_string_buffer(nbytes)
+    assert lib.nb_gemv_batch_plan(arr, 2, buf, nbytes) == _lib.NB_OK
+    assert lib.nb_gemv_batch_plan(arr, 2, buf, nbytes - 1) == _lib.NB_EINVAL
+    assert lib.nb_gemv_batch_plan(arr, -1, buf, nbytes) == _lib.NB_EINVAL
+    for bad, st in ((Item(FAKE, FAKE, FAKE, FAKE, 32, 200), _lib.NB_EUNSUPPORTED),
+                    (Item(FAKE, FAKE, FAKE, FAKE, 32, 8320), _lib.NB_EUNSUPPORTED),
+                    (Item(FAKE + 8, FAKE, FAKE, FAKE, 32, 256), _lib.NB_EALIGN),
+                    (Item(FAKE, None, FAKE, FAKE, 32, 256), _lib.NB_EINVAL),
+                    (Item(FAKE, FAKE, FAKE, FAKE, -1, 256), _lib.NB_EINVAL)):
+        one = (Item * 1)(bad)
+        assert lib.nb_gemv_batch_plan(one, 1, buf, nbytes) == st
+        assert lib.nb_gemv_batched(one, FAKE, 1, _lib.NB_F32, None) == st
+    assert lib.nb_gemv_batched(arr, None, 2, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert lib.nb_gemv_batched(arr, FAKE, 2, 7, None) == _lib.NB_EINVAL
+    empty = (Item * 1)(Item(None, None, None, None, 0, 256))
+    assert lib.nb_gemv_batched(empty, None, 1, _lib.NB_F32, None) == _lib.NB_OK

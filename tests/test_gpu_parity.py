@@ -98,6 +98,21 @@ def run_gemv(dev, x, p, cb, N, K, bits, bs, out_dtype=torch.float32):
                     N, K, bits=bits, block_size=bs, out_dtype=out_dtype)
 
 
+def ref_weights(idx, cb, bs, N, K, xdt):
+    """Dequantized W as the GEMV contract defines it: exact fp32 for fp32 x,
+    rounded to bf16 (torch's cast, pinned in tests/test_oracle.py) for bf16 x."""
+    w = O.dequant(idx, cb, bs, N * K).reshape(N, K)
+    if xdt == torch.bfloat16:
+        w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+    return w
+
+
+def ref_gemv(x, idx, cb, bs, N, K):
+    """fp64 brute force over exactly the operands the kernel multiplies."""
+    w = ref_weights(idx, cb, bs, N, K, x.dtype)
+    return O.matmul_f64(x.float().reshape(-1, K).numpy(), w)
+
+
 def test_golden_gemv_exact(dev, golden):
     for g in golden["gemv"]:
         p = np.frombuffer(bytes.fromhex(g["packed_hex"]), np.uint8).copy()
@@ -116,15 +131,61 @@ def test_gemv_3bit_2p2b_shapes(dev, N, K, xdt):
     idx, p, cb = random_layer(N, K, 3, 8, 128, N * 3 + K)
     x = torch.randn(K, generator=torch.Generator().manual_seed(N)).to(xdt)
     y = run_gemv(dev, x, p, cb, N, K, 3, 128).cpu().numpy()
-    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
-    ref = O.matmul_f64(x.float().numpy(), w)[0]
+    ref = ref_gemv(x, idx, cb, 128, N, K)[0]
     assert rel(y, ref) <= REL_F32, rel(y, ref)
+    # the reference kernel's own fp32 arithmetic (cuda_kernel.py:53-81) ...
+    k1 = O.matvec_3bit_k1(x.float().numpy(), p, cb, N, K)
     if xdt == torch.bfloat16:
+        # ... and the reference's bf16 path (eval_ppl.py:149-174) agree
         ref16 = O.torch_packed_linear_bf16(x, torch.from_numpy(p), torch.from_numpy(cb), N, K)
         assert rel(y, ref16.float().numpy()) <= REL_BF16
-    # the reference kernel's own fp32 order agrees too
-    k1 = O.matvec_3bit_k1(x.float().numpy(), p, cb, N, K)
-    assert rel(y, k1) <= REL_F32
+        assert rel(y, k1) <= REL_BF16
+    else:
+        assert rel(y, k1) <= REL_F32
+
+
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("N,K", [(2560, 2560), (6912, 2560), (2560, 6912)])
+def test_gemv_skinny_bf16(dev, M, N, K):
+    """Config 2: M activation rows share one pass over the packed weights."""
+    note(f"skinny gemv M={M} N={N} K={K}")
+    idx, p, cb = random_layer(N, K, 3, 8, 128, M * 7 + N + K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+    y = run_gemv(dev, x, p, cb, N, K, 3, 128).cpu().numpy()
+    ref = ref_gemv(x, idx, cb, 128, N, K)
+    assert y.shape == (M, N)
+    for m in range(M):
+        assert rel(y[m], ref[m]) <= REL_F32, (m, rel(y[m], ref[m]))
+
+
+def test_gemv_strided_rows_bf16(dev):
+    """x rows with a stride larger than K (a view into a wider buffer)."""
+    N, K, M = 1000, 2560, 6
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 77)
+    big = torch.randn(M, K + 64, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    x = big[:, :K]
+    y = ops.gemv(x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K)
+    xv = big.to(dev)[:, :K]
+    assert xv.stride(0) == K + 64
+    y2 = ops.gemv(xv, torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K)
+    ref = ref_gemv(x.contiguous(), idx, cb, 128, N, K)
+    assert rel(y.cpu(), ref) <= REL_F32 and rel(y2.cpu(), ref) <= REL_F32
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_mfma_and_generic_agree_bf16(dev, M):
+    """The MFMA kernel and the generic kernel (reached through a misaligned x)
+    compute the same bf16-weight product."""
+    N, K = 2560, 6912
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 500 + M)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
+    buf = torch.empty(M * K + 1, dtype=torch.bfloat16, device=dev)
+    x_mis = buf[1:].view(M, K)
+    x_mis.copy_(x)
+    y_mfma = ops.gemv(x, pt, ct, N, K)
+    y_gen = ops.gemv(x_mis, pt, ct, N, K)
+    assert rel(y_gen.cpu(), y_mfma.cpu()) <= 1e-5
 
 
 @pytest.mark.parametrize("ne,bs", [(4, 64), (4, 128), (4, 256), (8, 64), (8, 128),
@@ -136,7 +197,7 @@ def test_gemv_bits_block_sweep(dev, ne, bs, N, K):
     idx, p, cb = random_layer(N, K, bits, ne, bs, ne * 1000 + bs + N)
     x = torch.randn(K, generator=torch.Generator().manual_seed(ne + bs)).to(torch.bfloat16)
     y = run_gemv(dev, x, p, cb, N, K, bits, bs).cpu().numpy()
-    ref = O.matmul_f64(x.float().numpy(), O.dequant(idx, cb, bs, N * K).reshape(N, K))[0]
+    ref = ref_gemv(x, idx, cb, bs, N, K)[0]
     assert rel(y, ref) <= REL_F32
 
 
@@ -208,14 +269,14 @@ def test_packed_linear_api(dev):
     layer = PackedLinear.from_packed(idx.reshape(-1, 128), cb, (N, K), device=dev)
     assert torch.equal(layer.packed_indices.cpu(), torch.from_numpy(p))
     assert layer.out_features == N and layer.in_features == K
-    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
-    for shape in [(K,), (1, K), (1, 1, K), (3, K), (2, 5, K), (40, K)]:
-        note(f"PackedLinear x{shape}")
-        x = torch.randn(*shape, generator=torch.Generator().manual_seed(len(shape)))
-        y = layer(x.to(dev))
-        assert y.dtype == torch.float32 and y.shape == (*shape[:-1], N)
-        ref = O.matmul_f64(x.reshape(-1, K).numpy(), w)
-        assert rel(y.cpu().reshape(-1, N), ref) <= REL_F32
+    for xdt in (torch.float32, torch.bfloat16):
+        for shape in [(K,), (1, K), (1, 1, K), (3, K), (2, 5, K), (40, K)]:
+            note(f"PackedLinear x{shape} {xdt}")
+            x = torch.randn(*shape, generator=torch.Generator().manual_seed(len(shape))).to(xdt)
+            y = layer(x.to(dev))
+            assert y.dtype == torch.float32 and y.shape == (*shape[:-1], N)
+            ref = ref_gemv(x.reshape(-1, K), idx, cb, 128, N, K)
+            assert rel(y.cpu().reshape(-1, N), ref) <= REL_F32
 
 
 def test_kernels_mirror(dev):
@@ -261,7 +322,7 @@ def test_synth_layer_all_shapes_vs_f64(dev):
         idx = lay.indices.cpu().numpy()
         cb = lay.codebook.cpu().numpy()
         assert np.array_equal(lay.packed.cpu().numpy(), O.pack(idx, 3))
-        ref = O.matmul_f64(x.float().cpu().numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
+        ref = ref_gemv(x.cpu(), idx, cb, 128, N, K)[0]
         assert rel(y, ref) <= REL_F32
 
 
@@ -281,3 +342,79 @@ def test_full_model_properties(dev):
                 y2 = ops.gemv(x2, lay.packed, lay.codebook, N, K)
                 y12 = ops.gemv(x1 + x2, lay.packed, lay.codebook, N, K)
                 assert rel(y12.cpu(), (y1 + y2).cpu()) <= 1e-5
+
+
+# --------------------------------------------------------------------------
+# batched streaming GEMV (nb_gemv_batched)
+# --------------------------------------------------------------------------
+
+def test_batched_matches_single_and_f64(dev):
+    """Mixed shapes, ragged N, an empty item, bf16 output: every item equals
+    its own fp64 reference and the single-call nb_gemv."""
+    shapes = [(2560, 2560), (100, 2560), (6912, 2560), (0, 2560), (2560, 6912), (17, 128),
+              (1000, 6912), (16, 256)]
+    items, refs, singles = [], [], []
+    for i, (N, K) in enumerate(shapes):
+        note(f"batched item {i} {N}x{K}")
+        idx, p, cb = random_layer(max(N, 1), K, 3, 8, 128, 900 + i)
+        x = torch.randn(K, generator=torch.Generator().manual_seed(i)).to(torch.bfloat16)
+        pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+        if N == 0:
+            pt, ct = pt[:16].clone(), ct[:0].reshape(0, 8).contiguous()
+        y = torch.full((N,), float("nan"), device=dev)
+        items.append((x.to(dev), pt, ct, y, N, K))
+        refs.append(ref_gemv(x, idx, cb, 128, N, K)[0] if N else None)
+        singles.append(ops.gemv(x.to(dev), pt, ct, N, K) if N else None)
+    batch = ops.GemvBatch(items)
+    batch.run()
+    for i, (x, pt, ct, y, N, K) in enumerate(items):
+        if N == 0:
+            continue
+        assert rel(y.cpu(), refs[i]) <= REL_F32, (i, rel(y.cpu(), refs[i]))
+        assert rel(y.cpu(), singles[i].cpu()) <= 1e-5
+    # bf16 outputs and a second run over the same table are stable
+    ys16 = [torch.empty(N, dtype=torch.bfloat16, device=dev) for (_, _, _, _, N, _) in items]
+    b16 = ops.GemvBatch([(x, p, c, y16, N, K) for (x, p, c, _, N, K), y16 in zip(items, ys16)])
+    b16.run()
+    b16.run()
+    for (x, p, c, y, N, K), y16 in zip(items, ys16):
+        if N:
+            assert torch.equal(y16.cpu(), y.cpu().to(torch.bfloat16))
+
+
+def test_batched_full_model_layer(dev):
+    """One layer's seven matmuls from the synthetic generator in one batch."""
+    mats = []
+    for j, (name, N, K) in enumerate(synth.LAYER_SHAPES):
+        lay = synth.make_layer(N, K, seed=700 + j, device=dev, keep_indices=True)
+        x = synth.make_activation(K, seed=800 + j, device=dev, dtype=torch.bfloat16)[0].contiguous()
+        mats.append((lay, x, torch.empty(N, device=dev)))
+    ops.GemvBatch([(x, l.packed, l.codebook, y, l.out_features, l.in_features)
+                   for l, x, y in mats]).run()
+    for l, x, y in mats:
+        ref = ref_gemv(x.cpu(), l.indices.cpu().numpy(), l.codebook.cpu().numpy(), 128,
+                       l.out_features, l.in_features)[0]
+        assert rel(y.cpu(), ref) <= REL_F32
+
+
+def test_batched_graph_replay(dev):
+    """Captured in a HIP graph and replayed several times, with eager work in
+    between, every replay reproduces the eager result."""
+    N, K = 2560, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 4242)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    x = torch.randn(K, device=dev).to(torch.bfloat16)
+    y = torch.empty(N, device=dev)
+    b = ops.GemvBatch([(x, pt, ct, y, N, K)])
+    b.run()
+    torch.cuda.synchronize()
+    eager = y.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        b.run()
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, eager)
