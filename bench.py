@@ -51,13 +51,18 @@ def parse():
     p = argparse.ArgumentParser(description=__doc__,
                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=100)
-    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--steps", type=int, default=500)
+    p.add_argument("--warmup", type=int, default=500)
     p.add_argument("--layers", type=int, default=26)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--schedules", default="batched,per_layer,decode",
                    help="comma list of schedules to time (batched is the reported value)")
-    p.add_argument("--cpu-reps", type=int, default=3)
+    p.add_argument("--cpu-reps", type=int, default=3, help="minimum CPU baseline passes")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="CPU baseline passes continue until this much time has been spent")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="also time a plain 1 GiB device copy (the yardstick that scales "
+                        "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     return p.parse_args()
 
 
@@ -126,6 +131,35 @@ def graph_time(run, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def copy_calibration(dev, steps, warmup):
+    """A plain device copy of 1 GiB (torch's copy kernel), timed like the
+    GEMV.  Its known byte counts (1 GiB read, 1 GiB written) are the scale for
+    the FETCH_SIZE / WRITE_SIZE counters read in the same profiled process."""
+    n = 2**30 // 4
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    ms = graph_time(lambda: dst.copy_(src), max(5, steps // 20), max(2, warmup // 20))
+    out = {"bytes_read": 2**30, "bytes_written": 2**30, "us": round(ms * 1e3, 2),
+           "GB_s": round(2 * 2**30 / ms / 1e6, 1)}
+    del src, dst
+    return out
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (profiles/traffic_<kernel>_config1.txt, key `traffic_bytes`), or
+    None when no such summary exists."""
+    path = os.path.join(ROOT, "profiles", f"traffic_{kernel}_config1.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def decode_launches(layers):
     """(x, packed, cb, y, N, K) of the 104 decode-step launches."""
     out = []
@@ -160,7 +194,7 @@ def spot_check(mats):
     return worst
 
 
-def cpu_baseline(mats, reps):
+def cpu_baseline(mats, reps, seconds):
     """The reference CPU path (unpack + gather + F.linear, restated in
     oracle.torch_packed_linear_f32) on layer 0's 7 matmuls."""
     from oracle import oracle as O
@@ -175,7 +209,8 @@ def cpu_baseline(mats, reps):
 
     once()
     times = []
-    for _ in range(reps):
+    t_start = time.perf_counter()
+    while len(times) < reps or time.perf_counter() - t_start < seconds:
         t0 = time.perf_counter()
         once()
         times.append(time.perf_counter() - t0)
@@ -190,7 +225,8 @@ def cpu_baseline(mats, reps):
         "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"layer 0 of config 1 (q, k, v, o, gate, up, down; {nbytes} B): torch CPU "
                    f"unpack+gather+F.linear (reference triton_kernel.py:258-275), x bf16 upcast "
-                   f"to fp32, median of {reps} after 1 warm-up = {t*1e3:.1f} ms; {threads} "
+                   f"to fp32, median of {len(times)} passes ({sum(times):.1f} s) after 1 warm-up "
+                   f"= {t*1e3:.1f} ms per pass; {threads} "
                    f"threads on {cpu_model or platform.processor()}"),
         "seconds_per_sample": round(t, 4),
     }
@@ -289,7 +325,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic("gemv_stream_kernel"),
             "kernel": "gemv_stream_kernel",
             "method": ("algorithmic bytes per launch (0.625 B/weight + x + y) / HIP-event time "
                        "per graph replay of the single launch, on the launch stream"),
@@ -297,11 +333,14 @@ def main():
         "schedules": results,
         "parity": {"spot_check_rel_err_vs_f64": err},
     }
+    if args.copy_calibration:
+        result["copy_calibration"] = copy_calibration(dev, args.steps, args.warmup)
+        log(f"[bench] copy calibration: {result['copy_calibration']}")
     if not args.no_cpu_baseline:
         log("[bench] timing CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline([layers[0][n] for n in
                                                ("q", "k", "v", "o", "gate", "up", "down")],
-                                              args.cpu_reps)
+                                              args.cpu_reps, args.cpu_seconds)
         log(f"[bench] cpu baseline {result['cpu_baseline']['value']} GB/s "
             f"({result['cpu_baseline']['cores']} threads)")
     print(json.dumps(result), flush=True)

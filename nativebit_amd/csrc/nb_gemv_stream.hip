@@ -32,7 +32,11 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
-constexpr int kWaves = 4;          // waves per workgroup (independent workers)
+// waves per workgroup (independent workers)
+#ifndef NB_STREAM_WAVES
+#define NB_STREAM_WAVES 4
+#endif
+constexpr int kWaves = NB_STREAM_WAVES;
 
 #ifndef NB_STREAM_WG_PER_CU
 #define NB_STREAM_WG_PER_CU 2
@@ -53,9 +57,25 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 // interleave low and high bytes into bf16x2 pairs.
 __device__ __forceinline__ u32x4_t lookup8(uint32_t g, uint32_t lo0, uint32_t lo1,
                                            uint32_t hi0, uint32_t hi1) {
-    const uint32_t h = __builtin_amdgcn_ubfe(g, 0, 16) | ((g << 4) & 0xFFFF0000u);
-    const uint32_t sa = (h & 0x00070007u) | ((h << 5) & 0x07000700u);
-    const uint32_t sb = ((h >> 6) & 0x00070007u) | ((h >> 1) & 0x07000700u);
+    // h = indices 0-3 in the low half, 4-7 in the high half (bits 0,3,6,9):
+    //   h  = bfi(0xffff, g, g << 4)
+    //   sa = (h & 0x00070007) | ((h << 5) & 0x07000700)   bytes (i0,i1,i4,i5)
+    //   sb = ((h >> 6) & 0x00070007) | ((h >> 1) & 0x07000700)   (i2,i3,i6,i7)
+    // Written as one asm block (VALU only, no memory) because the compiler
+    // otherwise rebuilds h in pieces and spends 11 ops instead of 9.
+    // (VOP3 forms take no literal on gfx9: the masks come in as SGPRs.)
+    uint32_t sa, sb, t0, t1;
+    asm("v_lshlrev_b32 %2, 4, %4\n\t"
+        "v_bfi_b32 %2, %5, %4, %2\n\t"
+        "v_lshlrev_b32 %3, 5, %2\n\t"
+        "v_and_b32 %0, %6, %2\n\t"
+        "v_and_or_b32 %0, %3, %7, %0\n\t"
+        "v_lshrrev_b32 %3, 1, %2\n\t"
+        "v_lshrrev_b32 %2, 6, %2\n\t"
+        "v_and_b32 %3, %7, %3\n\t"
+        "v_and_or_b32 %1, %2, %6, %3"
+        : "=&v"(sa), "=&v"(sb), "=&v"(t0), "=&v"(t1)
+        : "v"(g), "s"(0xffffu), "s"(0x00070007u), "s"(0x07000700u));
     const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sa);
     const uint32_t ha = __builtin_amdgcn_perm(hi1, hi0, sa);
     const uint32_t lb = __builtin_amdgcn_perm(lo1, lo0, sb);
