@@ -10,6 +10,7 @@
 #include <string.h>
 
 #include <mutex>
+#include <vector>
 
 #include "nb_internal.h"
 
@@ -207,6 +208,32 @@ int64_t nb_gemv_batch_table_bytes(int count) {
 
 }  // extern "C"
 
+int nb::build_stream_table(const nb_batch_item* items, int count, StreamProblem* out) {
+    int32_t begin = 0, step_begin = 0;
+    int n = 0;
+    for (int i = 0; i < count; ++i) {
+        const nb_batch_item& it = items[i];
+        if (it.N == 0) continue;
+        StreamProblem p;
+        memset(&p, 0, sizeof(p));
+        p.x = static_cast<const uint16_t*>(it.x);
+        p.packed = it.packed;
+        p.codebook = it.codebook;
+        p.y = it.y;
+        p.N = it.N;
+        p.K = it.K;
+        p.bpr = it.K / 128;
+        p.nsteps = (p.bpr + 3) / 4;
+        p.tiles = (it.N + 15) / 16;
+        p.tile_begin = begin;
+        p.step_begin = step_begin;
+        begin += p.tiles;
+        step_begin += p.tiles * p.nsteps;
+        out[n++] = p;
+    }
+    return n;
+}
+
 namespace {
 
 // Shared validation of batch items; fills total tiles and the largest K.
@@ -258,30 +285,8 @@ int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
     if (count > 0 && !table_host) return fail(NB_EINVAL, "%s: table_host is NULL", fn);
     // Items with N == 0 are left out; the table holds the others in order and
     // the unused tail of the table is zeroed.
-    StreamProblem* t = static_cast<StreamProblem*>(table_host);
     memset(table_host, 0, (size_t)nb_gemv_batch_table_bytes(count));
-    int32_t begin = 0, step_begin = 0;
-    int n = 0;
-    for (int i = 0; i < count; ++i) {
-        const nb_batch_item& it = items[i];
-        if (it.N == 0) continue;
-        StreamProblem p;
-        memset(&p, 0, sizeof(p));
-        p.x = static_cast<const uint16_t*>(it.x);
-        p.packed = it.packed;
-        p.codebook = it.codebook;
-        p.y = it.y;
-        p.N = it.N;
-        p.K = it.K;
-        p.bpr = it.K / 128;
-        p.nsteps = (p.bpr + 3) / 4;
-        p.tiles = (it.N + 15) / 16;
-        p.tile_begin = begin;
-        p.step_begin = step_begin;
-        begin += p.tiles;
-        step_begin += p.tiles * p.nsteps;
-        t[n++] = p;
-    }
+    build_stream_table(items, count, static_cast<StreamProblem*>(table_host));
     return NB_OK;
 }
 
@@ -306,7 +311,10 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
     }
     st = ensure_device();
     if (st) return st;
-    return launch_gemv_stream(static_cast<const StreamProblem*>(table_dev), nprob, (int)steps, mk,
+    // host copy of the table the caller uploaded (same items, same order)
+    std::vector<StreamProblem> host((size_t)nprob);
+    build_stream_table(items, count, host.data());
+    return launch_gemv_stream(static_cast<const StreamProblem*>(table_dev), host.data(), nprob,
                               y_dtype, static_cast<hipStream_t>(stream));
 }
 

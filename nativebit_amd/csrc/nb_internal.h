@@ -57,8 +57,23 @@ struct StreamProblem {
     int32_t pad;
 };
 
-int launch_gemv_stream(const StreamProblem* dev_probs, int nprob, int total_steps,
-                       int max_k, int y_dtype, hipStream_t stream);
+// Tile ranges of one streaming launch (kernel argument, by value): workgroup
+// g owns tiles [tile0[g], tile0[g+1]) of problems prob0[g] .. prob1[g].
+constexpr int kStreamMaxGroups = 256;
+struct StreamRanges {
+    int32_t tile0[kStreamMaxGroups + 1];
+    int32_t prob0[kStreamMaxGroups];
+    int32_t prob1[kStreamMaxGroups];
+};
+
+// Fills `out` (nprob entries) from the batch items with N > 0, in order;
+// returns nprob.
+int build_stream_table(const nb_batch_item* items, int count, StreamProblem* out);
+
+// Launches the streaming kernel over the problem table (device copy for the
+// kernel, host copy to plan the workgroup ranges).
+int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
+                       int nprob, int y_dtype, hipStream_t stream);
 
 // Kernel launchers (arguments already validated by nb_abi.cpp).
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
