@@ -209,7 +209,7 @@ int64_t nb_gemv_batch_table_bytes(int count) {
 }  // extern "C"
 
 int nb::build_stream_table(const nb_batch_item* items, int count, StreamProblem* out) {
-    int32_t begin = 0, step_begin = 0;
+    int32_t chunk_begin = 0;
     int n = 0;
     for (int i = 0; i < count; ++i) {
         const nb_batch_item& it = items[i];
@@ -223,12 +223,9 @@ int nb::build_stream_table(const nb_batch_item* items, int count, StreamProblem*
         p.N = it.N;
         p.K = it.K;
         p.bpr = it.K / 128;
-        p.nsteps = (p.bpr + 3) / 4;
-        p.tiles = (it.N + 15) / 16;
-        p.tile_begin = begin;
-        p.step_begin = step_begin;
-        begin += p.tiles;
-        step_begin += p.tiles * p.nsteps;
+        p.nchunks = (int32_t)(((int64_t)it.N * p.bpr + 63) / 64);
+        p.chunk_begin = chunk_begin;
+        chunk_begin += p.nchunks;
         out[n++] = p;
     }
     return n;
@@ -236,12 +233,13 @@ int nb::build_stream_table(const nb_batch_item* items, int count, StreamProblem*
 
 namespace {
 
-// Shared validation of batch items; fills total tiles and the largest K.
-int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* total_steps,
+// Shared validation of batch items; fills the total chunk count and the
+// largest K.
+int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* total_chunks,
                 int* max_k) {
     if (count < 0) return fail(NB_EINVAL, "%s: count=%d < 0", fn, count);
     if (count > 0 && !items) return fail(NB_EINVAL, "%s: items is NULL", fn);
-    int64_t steps = 0;
+    int64_t chunks = 0;
     int mk = 0;
     for (int i = 0; i < count; ++i) {
         const nb_batch_item& it = items[i];
@@ -251,6 +249,11 @@ int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* 
             return fail(NB_EUNSUPPORTED, "%s: item %d K=%d (needs K %% 128 == 0, 0 < K <= 8192)",
                         fn, i, it.K);
         }
+        // block numbers are exact in fp32 below 2^24 (the kernel's row split)
+        if ((int64_t)it.N * (it.K / 128) >= (1LL << 24)) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d has %lld blocks (limit 2^24)", fn, i,
+                        (long long)it.N * (it.K / 128));
+        }
         if (!it.x || !it.packed || !it.codebook || !it.y) {
             return fail(NB_EINVAL, "%s: item %d has a NULL pointer", fn, i);
         }
@@ -258,11 +261,11 @@ int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* 
             return fail(NB_EALIGN, "%s: item %d x/packed/codebook not 16-byte aligned", fn, i);
         }
         if (!aligned(it.y, 2)) return fail(NB_EALIGN, "%s: item %d y not 2-byte aligned", fn, i);
-        steps += (int64_t)((it.N + 15) / 16) * ((it.K / 128 + 3) / 4);
+        chunks += ((int64_t)it.N * (it.K / 128) + 63) / 64;
         if (it.K > mk) mk = it.K;
     }
-    if (steps > INT32_MAX) return fail(NB_EUNSUPPORTED, "%s: %lld steps exceed int32", fn, (long long)steps);
-    *total_steps = steps;
+    if (chunks > INT32_MAX) return fail(NB_EUNSUPPORTED, "%s: %lld chunks exceed int32", fn, (long long)chunks);
+    *total_chunks = chunks;
     *max_k = mk;
     return NB_OK;
 }
@@ -274,9 +277,9 @@ extern "C" {
 int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
                        int64_t table_bytes) {
     const char* fn = "nb_gemv_batch_plan";
-    int64_t steps = 0;
+    int64_t chunks = 0;
     int mk = 0;
-    int st = check_batch(items, count, fn, &steps, &mk);
+    int st = check_batch(items, count, fn, &chunks, &mk);
     if (st) return st;
     if (table_bytes < nb_gemv_batch_table_bytes(count)) {
         return fail(NB_EINVAL, "%s: table of %lld bytes, %lld needed", fn, (long long)table_bytes,
@@ -293,12 +296,12 @@ int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
 int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count, int y_dtype,
                     void* stream) {
     const char* fn = "nb_gemv_batched";
-    int64_t steps = 0;
+    int64_t chunks = 0;
     int mk = 0;
-    int st = check_batch(items, count, fn, &steps, &mk);
+    int st = check_batch(items, count, fn, &chunks, &mk);
     if (st) return st;
     if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
-    if (steps == 0) return NB_OK;
+    if (chunks == 0) return NB_OK;
     if (!table_dev) return fail(NB_EINVAL, "%s: table_dev is NULL", fn);
     if (!aligned(table_dev, 8)) return fail(NB_EALIGN, "%s: table_dev not 8-byte aligned", fn);
     int nprob = 0;

@@ -2,31 +2,53 @@
 //
 //   for every problem p:  y_p[n] = sum_k x_p[k] * bf16(W_p[n][k])   (M = 1)
 //
-// One launch streams the packed weights of all problems.  The batch is cut
-// into 16-row tiles (tile t of problem p = rows 16t..16t+15, all of K),
-// numbered consecutively across problems.  Each workgroup owns a contiguous
-// tile range holding 1/G of all steps (a K=6912 tile costs 14 steps, a
-// K=2560 tile 5); inside it, its waves take tiles one at a time from a
-// counter in LDS.  (Static per-wave ranges leave half of the kernel's time
-// to one wave per SIMD: the arbiter favours the older of two waves, which
-// finishes its share in about half the time of the other.)  A tile is
-// computed by one wave from start to end -- full rows, no cross-wave
-// reduction, no barrier after the counter is set up -- so results do not
-// depend on which wave took which tile.
+// One launch streams the packed weights of all problems.  Each problem's
+// blocks (128 weights: 48 bytes of 3-bit indices, 32 bytes of fp32
+// codebook) are cut into chunks of 64 consecutive blocks -- 3 KiB of index
+// stream and 2 KiB of codebook, both contiguous in HBM -- numbered
+// consecutively across problems.
 //
-// Each tile is consumed in steps of 4 blocks (512 columns): lane l = q*16 + r
-// loads row r's block 4*step + q (48 bytes of indices, 32 bytes of fp32
-// codebook), turns its 128 weights into 16 bf16 MFMA A-operands with the
-// register byte-plane lookup of nb_gemv_mfma.hip, and multiplies them by
-// x (B operand, from the wave's own LDS copy of x_p) with
-// v_mfma_f32_16x16x32_bf16.  The loads of the next two steps -- which may
-// belong to the next tile or the next problem -- are in flight while the
-// current step is consumed, so HBM requests stay in flight across tile
-// boundaries.
+// Memory side.  A wave loads a chunk with five global_load_lds_dwordx4
+// (direct-to-LDS) instructions, each covering one contiguous KiB, marked
+// non-temporal: the access shape under which MI355X streams at about
+// 7 TB/s (a 16-rows x 4-blocks tile pattern read into registers stays near
+// 5.7 TB/s even with all arithmetic removed).  Each wave owns a ring of
+// NB_STREAM_DEPTH chunk slots in LDS; a slot is refilled as soon as its
+// bytes are in registers, so NB_STREAM_DEPTH chunks per wave are in flight
+// while one is computed.
+//
+// Compute side.  Lane l takes block l of the chunk.  Its 48 index bytes are
+// four 12-byte units of 32 indices.  Index j of a unit starts at bit 3j, so
+// bytes 0,3,6,9 of a unit hold indices starting at bit offsets 0 and 3 of
+// the byte (and the low bits of one more), bytes 1,4,7,10 at offsets 1 and
+// 4, bytes 2,5,8,11 at 2 and 5.  v_perm_b32 gathers each class into one
+// dword, and a shift and a mask then yield four indices, one per byte: the
+// selector bytes of a v_perm_b32 lookup into the block's codebook, kept as
+// byte planes of its bf16-rounded entries (low bytes of entries 0-7, high
+// bytes of entries 0-7).  Eight selectors per unit (25 VALU ops for 32
+// indices), four v_perm_b32 per selector (two lookups, two interleaves),
+// give 4 bf16 weights -- indices o, o+8, o+16, o+24 of the unit -- for one
+// v_mfma_f32_4x4x4_16b_bf16.  The activations are staged in LDS in the same
+// order.  In that instruction lane 4b+i supplies row i of block b's A and
+// column i of its B, and the diagonal D[b][i][i] -- lane 4b+i, accumulator
+// i -- is the lane's own 4-term dot product: every lane accumulates a
+// private dot product, so a lane can hold any block of any row.
+//
+// Row sums.  A row of bpr <= 64 blocks lies in at most two consecutive
+// chunks.  Lanes of a quad that share a row add their dot products in a
+// fixed order (DPP); the quad's sum, or each lane's own value where the
+// quad spans a row boundary, goes by LDS atomic to part[row][s], s = 0 in
+// the chunk where the row starts and 1 in the next.  Each slot receives the
+// lanes of one instruction of one wave, and y[row] = part[row][0] +
+// part[row][1], so results do not depend on which wave took which chunk.
+// Workgroup ranges start and end on row boundaries, so no row is shared
+// between workgroups; inside a workgroup waves take chunks one at a time
+// from a counter in LDS.
 //
 // Weights are rounded to bf16 (RNE) as in the reference's bf16 path
 // (inference/eval_ppl.py:149-174); accumulation is fp32.
 #include <algorithm>
+#include <numeric>
 #include <utility>
 #include <vector>
 
@@ -36,19 +58,36 @@
 namespace nb {
 namespace {
 
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
-// waves per workgroup (two per SIMD)
+// waves per workgroup and chunks in flight per wave
 #ifndef NB_STREAM_WAVES
 #define NB_STREAM_WAVES 8
 #endif
-constexpr int kWaves = NB_STREAM_WAVES;
-
+#ifndef NB_STREAM_DEPTH
+#define NB_STREAM_DEPTH 2
+#endif
 #ifndef NB_STREAM_WG_PER_CU
 #define NB_STREAM_WG_PER_CU 1
 #endif
+constexpr int kWaves = NB_STREAM_WAVES;
+constexpr int kDepth = NB_STREAM_DEPTH;
+static_assert(kDepth == 2 || kDepth == 3, "ring depth 2 or 3");
+
+constexpr int kChunkBlocks = 64;
+constexpr int kChunkIdxBytes = kChunkBlocks * 48;  // 3 KiB
+constexpr int kChunkCbBytes = kChunkBlocks * 32;   // 2 KiB
+constexpr int kSlotBytes = kChunkIdxBytes + kChunkCbBytes;
+constexpr int kLoadsPerChunk = 5;
+
+// Index offset o of selector s inside a 32-index unit: selector s yields
+// indices o, o+8, o+16, o+24 (see the file comment).
+__host__ __device__ constexpr int sel_offset(int s) {
+    return s == 0 ? 0 : s == 1 ? 1 : s == 2 ? 3 : s == 3 ? 4 : s == 4 ? 6 : s == 5 ? 7 : s == 6 ? 2 : 5;
+}
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
@@ -58,170 +97,58 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, v);
 }
 
-// 8 bf16 weights (natural order) of one 24-bit index group from the byte
-// planes of the block's codebook.  Two selectors of four 3-bit indices (one
-// per byte) are built in 9 VALU ops; v_perm_b32 on the low-byte and
-// high-byte planes looks up four entries at once, and two more v_perm_b32
-// interleave low and high bytes into bf16x2 pairs.
-__device__ __forceinline__ u32x4_t lookup8(uint32_t g, uint32_t lo0, uint32_t lo1,
-                                           uint32_t hi0, uint32_t hi1) {
-    // h = indices 0-3 in the low half, 4-7 in the high half (bits 0,3,6,9):
-    //   h  = bfi(0xffff, g, g << 4)
-    //   sa = (h & 0x00070007) | ((h << 5) & 0x07000700)   bytes (i0,i1,i4,i5)
-    //   sb = ((h >> 6) & 0x00070007) | ((h >> 1) & 0x07000700)   (i2,i3,i6,i7)
-    // Written as one asm block (VALU only, no memory) because the compiler
-    // otherwise rebuilds h in pieces and spends 11 ops instead of 9.
-    // (VOP3 forms take no literal on gfx9: the masks come in as SGPRs.)
-    uint32_t sa, sb, t0, t1;
-    asm("v_lshlrev_b32 %2, 4, %4\n\t"
-        "v_bfi_b32 %2, %5, %4, %2\n\t"
-        "v_lshlrev_b32 %3, 5, %2\n\t"
-        "v_and_b32 %0, %6, %2\n\t"
-        "v_and_or_b32 %0, %3, %7, %0\n\t"
-        "v_lshrrev_b32 %3, 1, %2\n\t"
-        "v_lshrrev_b32 %2, 6, %2\n\t"
-        "v_and_b32 %3, %7, %3\n\t"
-        "v_and_or_b32 %1, %2, %6, %3"
-        : "=&v"(sa), "=&v"(sb), "=&v"(t0), "=&v"(t1)
-        : "v"(g), "s"(0xffffu), "s"(0x00070007u), "s"(0x07000700u));
-    const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sa);
-    const uint32_t ha = __builtin_amdgcn_perm(hi1, hi0, sa);
-    const uint32_t lb = __builtin_amdgcn_perm(lo1, lo0, sb);
-    const uint32_t hb = __builtin_amdgcn_perm(hi1, hi0, sb);
-    u32x4_t w;
-    w.x = __builtin_amdgcn_perm(ha, la, 0x05010400u);
-    w.y = __builtin_amdgcn_perm(hb, lb, 0x05010400u);
-    w.z = __builtin_amdgcn_perm(ha, la, 0x07030602u);
-    w.w = __builtin_amdgcn_perm(hb, lb, 0x07030602u);
-    return w;
+// The eight selectors of one 12-byte unit (d0, d1, d2): selector s holds
+// indices sel_offset(s) + 8k (k = 0..3), one per byte.
+__device__ __forceinline__ void unit_selectors(uint32_t d0, uint32_t d1, uint32_t d2,
+                                               uint32_t (&sel)[8]) {
+    const uint32_t M = 0x07070707u;
+    // T = bytes 0,3,6,9; U = bytes 1,4,7,10; E = bytes 2,5,8,11
+    const uint32_t t = __builtin_amdgcn_perm(d2, __builtin_amdgcn_perm(d1, d0, 0x00060300u),
+                                             0x05020100u);
+    const uint32_t u = __builtin_amdgcn_perm(d2, __builtin_amdgcn_perm(d1, d0, 0x00070401u),
+                                             0x06020100u);
+    const uint32_t e = __builtin_amdgcn_perm(d2, __builtin_amdgcn_perm(d1, d0, 0x00000502u),
+                                             0x07040100u);
+    sel[0] = t & M;                 // bit offset 0 of T bytes
+    sel[1] = (t >> 3) & M;          // offset 3
+    sel[2] = (u >> 1) & M;          // offset 1 of U bytes
+    sel[3] = (u >> 4) & M;          // offset 4
+    sel[4] = (e >> 2) & M;          // offset 2 of E bytes
+    sel[5] = (e >> 5) & M;          // offset 5
+    // bits 6-7 of a T byte + bit 0 of the next (U) byte
+    sel[6] = ((t >> 6) & 0x03030303u) | ((u << 2) & 0x04040404u);
+    // bit 7 of a U byte + bits 0-1 of the next (E) byte
+    sel[7] = ((u >> 7) & 0x01010101u) | ((e << 1) & 0x06060606u);
 }
 
-template <int J>
-__device__ __forceinline__ uint32_t group24(const uint32_t (&d)[12]) {
-    constexpr int bit = J * 24;
-    constexpr int w = bit >> 5;
-    constexpr int off = bit & 31;
-    if constexpr (off == 0) {
-        return d[w];
-    } else if constexpr (off + 24 <= 32) {
-        return d[w] >> off;
-    } else {
-        return __builtin_amdgcn_alignbit(d[w + 1], d[w], off);
-    }
+__device__ __forceinline__ f32x4_t mfma44(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
+                                          f32x4_t c) {
+    u32x2_t a = {a0, a1}, b = {b0, b1};
+    return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(bf16x4_t, a),
+                                                 __builtin_bit_cast(bf16x4_t, b), c, 0, 0, 0);
 }
 
-// One lane's loads of one step: 48 bytes of indices, 32 bytes of codebook.
-struct Regs {
-    u32x4_t d0, d1, d2, c0, c1;
-};
-
-// The three register sets of the prefetch ring sit in fixed VGPRs
-// (v[100:119], v[120:139], v[140:159]); their loads are issued with inline
-// asm and waited for with an explicit s_waitcnt vmcnt.  Left to itself, the
-// compiler moves a set that is still in flight into other registers in one
-// of the three unrolled copies of the step, and a move of an in-flight
-// register must first wait for it: that drains the ring every third step.
-// With the sets pinned, nothing touches a set between its load and its wait.
-// The loop issues no other vector-memory instruction, so the count is exact:
-// when a set is consumed, it and the two sets issued after it -- 15 loads --
-// are the only ones outstanding.
-#define NB_RING_LOAD(R0, R1, R2, R3, R4)                                                      \
-    __device__ __forceinline__ void load_set(const uint8_t* p, const float* c, Regs& s) {     \
-        asm volatile("global_load_dwordx4 %0, %1, off" : "={v[" #R0 "]}"(s.d0) : "v"(p));          \
-        asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "={v[" #R1 "]}"(s.d1) : "v"(p)); \
-        asm volatile("global_load_dwordx4 %0, %1, off offset:32" : "={v[" #R2 "]}"(s.d2) : "v"(p)); \
-        asm volatile("global_load_dwordx4 %0, %1, off" : "={v[" #R3 "]}"(s.c0) : "v"(c));          \
-        asm volatile("global_load_dwordx4 %0, %1, off offset:16" : "={v[" #R4 "]}"(s.c1) : "v"(c)); \
-    }                                                                                          \
-    __device__ __forceinline__ void wait_set(Regs& s) {                                        \
-        asm volatile("s_waitcnt vmcnt(10)"                                                     \
-                     : "+{v[" #R0 "]}"(s.d0), "+{v[" #R1 "]}"(s.d1), "+{v[" #R2 "]}"(s.d2),       \
-                       "+{v[" #R3 "]}"(s.c0), "+{v[" #R4 "]}"(s.c1));                            \
-    }
-
-namespace set0 { NB_RING_LOAD(100:103, 104:107, 108:111, 112:115, 116:119) }
-namespace set1 { NB_RING_LOAD(120:123, 124:127, 128:131, 132:135, 136:139) }
-namespace set2 { NB_RING_LOAD(140:143, 144:147, 148:151, 152:155, 156:159) }
-#undef NB_RING_LOAD
-
-// Waits for every set (the loads issued past the wave's last step land
-// before their registers are released).
-__device__ __forceinline__ void wait_all(Regs& a, Regs& b, Regs& c) {
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+{v[100:103]}"(a.d0), "+{v[104:107]}"(a.d1), "+{v[108:111]}"(a.d2),
-                   "+{v[112:115]}"(a.c0), "+{v[116:119]}"(a.c1),
-                   "+{v[120:123]}"(b.d0), "+{v[124:127]}"(b.d1), "+{v[128:131]}"(b.d2),
-                   "+{v[132:135]}"(b.c0), "+{v[136:139]}"(b.c1),
-                   "+{v[140:143]}"(c.d0), "+{v[144:147]}"(c.d1), "+{v[148:151]}"(c.d2),
-                   "+{v[152:155]}"(c.c0), "+{v[156:159]}"(c.c1));
-}
-
-template <int J>
-__device__ __forceinline__ void mfma_groups(const uint32_t (&d)[12], uint32_t lo0, uint32_t lo1,
-                                            uint32_t hi0, uint32_t hi1,
-                                            const u32x4_t (&bv)[16], f32x4_t& acc0,
-                                            f32x4_t& acc1) {
-    if constexpr (J < 16) {
-        const u32x4_t a = lookup8(group24<J>(d), lo0, lo1, hi0, hi1);
-        const u32x4_t b = bv[J];
-        // two accumulators halve the dependent-MFMA chain
-        if constexpr (J % 2 == 0) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                           __builtin_bit_cast(bf16x8_t, b),
-                                                           acc0, 0, 0, 0);
-        } else {
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                           __builtin_bit_cast(bf16x8_t, b),
-                                                           acc1, 0, 0, 0);
-        }
-        mfma_groups<J + 1>(d, lo0, lo1, hi0, hi1, bv, acc0, acc1);
-    }
-}
-
-__device__ __forceinline__ void consume(const Regs& s, bool live,
-                                        const u32x4_t* __restrict__ bsrc, f32x4_t& acc0,
-                                        f32x4_t& acc1) {
-    // all 16 B operands (x at this lane's 128 columns) requested at once, so
-    // their LDS latency overlaps the codebook planes and the first lookups
-    u32x4_t bv[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) bv[j] = bsrc[j];
-    // keep the scheduler from sinking the reads back next to their MFMAs
-    __builtin_amdgcn_sched_barrier(0);
-    const uint32_t p0 = pack_bf16x2(__uint_as_float(s.c0.x), __uint_as_float(s.c0.y));
-    const uint32_t p1 = pack_bf16x2(__uint_as_float(s.c0.z), __uint_as_float(s.c0.w));
-    const uint32_t p2 = pack_bf16x2(__uint_as_float(s.c1.x), __uint_as_float(s.c1.y));
-    const uint32_t p3 = pack_bf16x2(__uint_as_float(s.c1.z), __uint_as_float(s.c1.w));
-    uint32_t lo0 = __builtin_amdgcn_perm(p1, p0, 0x06040200u);
-    uint32_t hi0 = __builtin_amdgcn_perm(p1, p0, 0x07050301u);
-    uint32_t lo1 = __builtin_amdgcn_perm(p3, p2, 0x06040200u);
-    uint32_t hi1 = __builtin_amdgcn_perm(p3, p2, 0x07050301u);
-    lo0 = live ? lo0 : 0u;
-    hi0 = live ? hi0 : 0u;
-    lo1 = live ? lo1 : 0u;
-    hi1 = live ? hi1 : 0u;
-    const uint32_t d[12] = {s.d0.x, s.d0.y, s.d0.z, s.d0.w, s.d1.x, s.d1.y,
-                            s.d1.z, s.d1.w, s.d2.x, s.d2.y, s.d2.z, s.d2.w};
-    mfma_groups<0>(d, lo0, lo1, hi0, hi1, bv, acc0, acc1);
-}
-
-// One problem of the workgroup's range as the step loop reads it, copied
+// One problem of the workgroup's range as the chunk loop reads it, copied
 // into LDS at set-up (64 bytes).
 struct ProbL {
     const uint8_t* packed;
     const float* codebook;
     void* y;
-    int32_t N, K, bpr, nsteps, tiles, tile_begin;
-    int32_t x_off;  // byte offset of this problem's x in the LDS x region
-    int32_t pad[3];
+    int32_t N, bpr, nchunks, chunk_begin;
+    int32_t x_off;   // byte offset of this problem's x (permuted) in LDS
+    int32_t y_off;   // float offset of its (part0, part1) row pairs in LDS
+    int32_t row_a;   // first row of this problem in the range
+    int32_t row_b;   // one past the last row
+    int32_t pad[2];
 };
 static_assert(sizeof(ProbL) == 64, "ProbL is 64 bytes");
 
-// The same fields in scalar registers.
+// The fields the loop needs, in scalar registers.
 struct Prob {
     const uint8_t* packed;
     const float* codebook;
-    int N, bpr, nsteps, tiles, tile_begin, x_off;
+    int nblocks, bpr, chunk_begin, chunk_end, x_off, y_off, row_a;
+    float inv_bpr;
 };
 
 template <typename T>
@@ -236,21 +163,71 @@ __device__ __forceinline__ void read_prob(const ProbL* pl, int li, Prob& P) {
     const ProbL& s = pl[li];
     P.packed = uniform_ptr(s.packed);
     P.codebook = uniform_ptr(s.codebook);
-    P.N = __builtin_amdgcn_readfirstlane(s.N);
+    const int N = __builtin_amdgcn_readfirstlane(s.N);
     P.bpr = __builtin_amdgcn_readfirstlane(s.bpr);
-    P.nsteps = __builtin_amdgcn_readfirstlane(s.nsteps);
-    P.tiles = __builtin_amdgcn_readfirstlane(s.tiles);
-    P.tile_begin = __builtin_amdgcn_readfirstlane(s.tile_begin);
+    P.nblocks = N * P.bpr;
+    P.chunk_begin = __builtin_amdgcn_readfirstlane(s.chunk_begin);
+    P.chunk_end = P.chunk_begin + __builtin_amdgcn_readfirstlane(s.nchunks);
     P.x_off = __builtin_amdgcn_readfirstlane(s.x_off);
+    P.y_off = __builtin_amdgcn_readfirstlane(s.y_off);
+    P.row_a = __builtin_amdgcn_readfirstlane(s.row_a);
+    P.inv_bpr = 1.0f / (float)P.bpr;
 }
 
-// Where one loaded register set belongs: problem (index in the workgroup's
-// range), tile inside it, step inside the tile.  `valid` is false for loads
-// issued after the wave ran out of tiles (they repeat the last address and
-// are never consumed).
+// Where one ring slot's chunk belongs.  `valid` is false for loads issued
+// after the wave ran out of chunks (they repeat the last address and are
+// never consumed).
 struct Meta {
-    int li, tile, step;
+    int li, lc;
     bool valid;
+};
+
+// One direct-to-LDS load: every lane reads 16 bytes at src + OFF, and lane
+// i's bytes land at LDS byte address lds + OFF + 16 i (the instruction
+// offset applies to both addresses).  Issued as inline asm so the compiler
+// does not track it: it would otherwise make every later LDS atomic wait
+// for all ring loads (the ring and the counters share one LDS array),
+// draining the prefetch at each chunk.  Reads of a slot are ordered after
+// its loads by wait_vm.
+template <int OFF>
+__device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off offset:%2 nt"
+                 :
+                 : "s"(lds), "v"(src), "n"(OFF)
+                 : "memory", "m0");
+}
+
+// Waits until at most N vector-memory operations of this wave are
+// outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// Waits for every LDS operation of this wave (a slot's reads must be done
+// before the slot is refilled).
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory"); }
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) T*)p;
+}
+
+// float DPP move within a quad (quad_perm control)
+template <int CTRL>
+__device__ __forceinline__ float quad_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int quad_mov_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+constexpr int quad_perm(int a, int b, int c, int d) { return a | (b << 2) | (c << 4) | (d << 6); }
+
+// One lane's bytes of one chunk.
+struct SlotRegs {
+    u32x4_t d0, d1, d2, c0, c1;
 };
 
 __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
@@ -258,251 +235,368 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int r = lane & 15;
-    const int q = lane >> 4;
+    const int wave = tid >> 6;
 
-    // ---- set-up: the workgroup's tiles, problems, x vectors and counter ----
+    // ---- set-up: the workgroup's chunks, problems, x vectors and counter --
     const int g = blockIdx.x;
-    const int T0 = ranges.tile0[g];
-    const int T1 = ranges.tile0[g + 1];
+    const int C0 = ranges.chunk0[g];
+    const int C1 = ranges.chunk0[g + 1];
     const int p0 = ranges.prob0[g];
     const int np = ranges.prob1[g] - p0 + 1;
     ProbL* pl = reinterpret_cast<ProbL*>(smem);
-    unsigned char* xregion = smem + np * (int)sizeof(ProbL);
-    int x_bytes = 0;  // every thread sums the K of the range (few problems)
-    for (int i = 0; i < np; ++i) x_bytes += probs[p0 + i].K * 2;
-    float* ybuf = reinterpret_cast<float*>(xregion + x_bytes);
-    int* next_tile = reinterpret_cast<int*>(ybuf + (T1 - T0) * 16);
-    if (tid < np) {
-        const StreamProblem& s = probs[p0 + tid];
-        ProbL d;
-        d.packed = s.packed;
-        d.codebook = s.codebook;
-        d.y = s.y;
-        d.N = s.N;
-        d.K = s.K;
-        d.bpr = s.bpr;
-        d.nsteps = s.nsteps;
-        d.tiles = s.tiles;
-        d.tile_begin = s.tile_begin;
-        int off = 0;
-        for (int i = 0; i < tid; ++i) off += probs[p0 + i].K * 2;
-        d.x_off = off;
-        d.pad[0] = d.pad[1] = d.pad[2] = 0;
-        pl[tid] = d;
+    unsigned char* ring = smem + np * (int)sizeof(ProbL);
+    unsigned char* xregion = ring + kWaves * kDepth * kSlotBytes;
+    // every thread walks the range's problems (few) to lay out LDS
+    int x_bytes = 0, y_floats = 0;
+    for (int i = 0; i < np; ++i) {
+        const StreamProblem& s = probs[p0 + i];
+        const int ca = max(C0, s.chunk_begin) - s.chunk_begin;
+        const int cb = min(C1, s.chunk_begin + s.nchunks) - s.chunk_begin;
+        const int ra = (int)(((int64_t)ca * kChunkBlocks) / s.bpr);
+        const int rb = min(s.N, (int)(((int64_t)cb * kChunkBlocks + s.bpr - 1) / s.bpr));
+        if (tid == i) {
+            ProbL d;
+            d.packed = s.packed;
+            d.codebook = s.codebook;
+            d.y = s.y;
+            d.N = s.N;
+            d.bpr = s.bpr;
+            d.nchunks = s.nchunks;
+            d.chunk_begin = s.chunk_begin;
+            d.x_off = x_bytes;
+            d.y_off = y_floats;
+            d.row_a = ra;
+            d.row_b = rb;
+            d.pad[0] = d.pad[1] = 0;
+            pl[i] = d;
+        }
+        x_bytes += s.K * 2;
+        y_floats += (rb - ra) * 2;
     }
+    float* ybuf = reinterpret_cast<float*>(xregion + x_bytes);
+    int* next_chunk = reinterpret_cast<int*>(ybuf + y_floats);
     {
+        // x of each problem in selector order: 16-byte unit j = 4u + m of
+        // column block c, at (j * bpr + c) * 16, holds the activations of
+        // selectors 2m and 2m+1 of unit u (4 bf16 each, in lookup order).
         int off = 0;
         for (int i = 0; i < np; ++i) {
-            const int K = probs[p0 + i].K;
-            const u32x4_t* src = reinterpret_cast<const u32x4_t*>(probs[p0 + i].x);
-            u32x4_t* dst = reinterpret_cast<u32x4_t*>(xregion + off);
-            for (int c = tid; c < K / 8; c += 64 * kWaves) dst[c] = *as_global(src + c);
-            off += K * 2;
+            const StreamProblem& s = probs[p0 + i];
+            for (int q = tid; q < s.bpr * 4; q += 64 * kWaves) {
+                const int c = q >> 2, u = q & 3;
+                const u32x4_t* src = reinterpret_cast<const u32x4_t*>(s.x + c * 128 + u * 32);
+                uint32_t w[16];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const u32x4_t t = *as_global(src + v);
+                    w[4 * v] = t.x;
+                    w[4 * v + 1] = t.y;
+                    w[4 * v + 2] = t.z;
+                    w[4 * v + 3] = t.w;
+                }
+                auto xs = [&](int k) -> uint32_t { return (w[k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int oa = sel_offset(2 * m), ob = sel_offset(2 * m + 1);
+                    u32x4_t o;
+                    o.x = xs(oa) | (xs(oa + 8) << 16);
+                    o.y = xs(oa + 16) | (xs(oa + 24) << 16);
+                    o.z = xs(ob) | (xs(ob + 8) << 16);
+                    o.w = xs(ob + 16) | (xs(ob + 24) << 16);
+                    *reinterpret_cast<u32x4_t*>(xregion + off + ((4 * u + m) * s.bpr + c) * 16) = o;
+                }
+            }
+            off += s.K * 2;
         }
     }
-    if (tid == 0) *next_tile = T0;
+    for (int e = tid; e < y_floats; e += 64 * kWaves) ybuf[e] = 0.f;
+    if (tid == 0) *next_chunk = C0;
     __syncthreads();
 
-    // ---- steady state: waves take tiles from the counter until none is left
+    // ---- steady state: waves take chunks from the counter until none is left
     auto grab = [&]() -> int {
         int t = 0;
-        if (lane == 0) t = atomicAdd(next_tile, 1);
+        if (lane == 0) t = atomicAdd(next_chunk, 1);
         return __builtin_amdgcn_readfirstlane(t);
     };
+    unsigned char* my_ring = ring + wave * kDepth * kSlotBytes;
+    const uint32_t my_ring_lds = lds_addr(my_ring);
 
-    int t_first = grab();
-    if (t_first < T1) {
-        // load cursor (runs two steps ahead of consumption)
+    const int c_first = grab();
+    if (c_first < C1) {
+        // load cursor (runs kDepth chunks ahead of computation)
         int li = 0;
         Prob LP;
         read_prob(pl, 0, LP);
-        while (t_first >= LP.tile_begin + LP.tiles) read_prob(pl, ++li, LP);
-        int ltile = t_first - LP.tile_begin, lstep = 0;
+        while (c_first >= LP.chunk_end) read_prob(pl, ++li, LP);
+        int lchunk = c_first;
         bool lvalid = true;
 
-        // Loads the step at the load cursor into s (always: after the last
-        // tile the cursor stays put and the load is a repeat), records where
-        // it belongs and moves the cursor on, taking a new tile when one ends.
-        auto issue = [&](auto load, Regs& s, Meta& m) {
-            const int row = ltile * 16 + r;
-            const int64_t lrow = row < LP.N ? row : LP.N - 1;
-            const int b = lstep * 4 + q;
-            const int bc = b < LP.bpr ? b : LP.bpr - 1;
-            const int64_t blk = lrow * LP.bpr + bc;
-            load(LP.packed + blk * 48, LP.codebook + blk * 8, s);
+        // Loads the chunk at the load cursor into ring slot `slot` (always:
+        // after the last chunk the cursor stays put and the load repeats),
+        // records where it belongs and moves the cursor to a new chunk.  In a
+        // problem's partial last chunk, lanes past the end of the stream
+        // re-read its last 16 bytes (their blocks are not live).
+        auto issue = [&](int slot, Meta& m) {
+            const int lc = lchunk - LP.chunk_begin;
+            const uint32_t dst = __builtin_amdgcn_readfirstlane(my_ring_lds + slot * kSlotBytes);
+            const uint8_t* ip = LP.packed + (int64_t)lc * kChunkIdxBytes + 16 * lane;
+            const uint8_t* cp = reinterpret_cast<const uint8_t*>(LP.codebook) +
+                                (int64_t)lc * kChunkCbBytes + 16 * lane;
+            if ((lc + 1) * kChunkBlocks <= LP.nblocks) {
+                dma16<0>(dst, ip);
+                dma16<1024>(dst, ip);
+                dma16<2048>(dst, ip);
+                dma16<0>(dst + kChunkIdxBytes, cp);
+                dma16<1024>(dst + kChunkIdxBytes, cp);
+            } else {
+                const uint8_t* ilast = LP.packed + (int64_t)LP.nblocks * 48 - 16;
+                const uint8_t* clast =
+                    reinterpret_cast<const uint8_t*>(LP.codebook) + (int64_t)LP.nblocks * 32 - 16;
+                dma16<0>(dst, min(ip, ilast));
+                dma16<0>(dst + 1024, min(ip + 1024, ilast));
+                dma16<0>(dst + 2048, min(ip + 2048, ilast));
+                dma16<0>(dst + kChunkIdxBytes, min(cp, clast));
+                dma16<0>(dst + kChunkIdxBytes + 1024, min(cp + 1024, clast));
+            }
             m.li = li;
-            m.tile = ltile;
-            m.step = lstep;
+            m.lc = lc;
             m.valid = lvalid;
             if (!lvalid) return;
-            if (++lstep == LP.nsteps) {
-                const int t = grab();
-                if (t >= T1) {
-                    lvalid = false;
-                    lstep = LP.nsteps - 1;  // repeat the last step's address
-                } else {
-                    lstep = 0;
-                    while (t >= LP.tile_begin + LP.tiles) read_prob(pl, ++li, LP);
-                    ltile = t - LP.tile_begin;
-                }
+            const int c = grab();
+            if (c >= C1) {
+                lvalid = false;  // repeat this chunk's addresses from now on
+            } else {
+                lchunk = c;
+                while (lchunk >= LP.chunk_end) read_prob(pl, ++li, LP);
             }
+        };
+
+        // This lane's 48 index bytes and 32 codebook bytes of a slot, in
+        // registers once wait_lds() has returned.
+        auto read_slot = [&](int slot) -> SlotRegs {
+            const unsigned char* src = my_ring + slot * kSlotBytes;
+            const u32x4_t* pi = reinterpret_cast<const u32x4_t*>(src + 48 * lane);
+            const u32x4_t* pc = reinterpret_cast<const u32x4_t*>(src + kChunkIdxBytes + 32 * lane);
+            SlotRegs r;
+            r.d0 = pi[0];
+            r.d1 = pi[1];
+            r.d2 = pi[2];
+            r.c0 = pc[0];
+            r.c1 = pc[1];
+            return r;
         };
 
         int ci = -1;  // problem whose fields are in CP
         Prob CP = {};
-        f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
 
-        auto step = [&](const Regs& s, const Meta& m) {
+        auto compute = [&](const SlotRegs& r, const Meta& m) {
             if (m.li != ci) {
                 read_prob(pl, m.li, CP);
                 ci = m.li;
             }
-            const int row = m.tile * 16 + r;
-            const int b = m.step * 4 + q;
-            const bool live = row < CP.N && b < CP.bpr;
-            const int bc = b < CP.bpr ? b : CP.bpr - 1;
-            const u32x4_t* xb = reinterpret_cast<const u32x4_t*>(xregion + CP.x_off) + bc * 16;
-            consume(s, live, xb, acc0, acc1);
-            if (m.step == CP.nsteps - 1) {
-                // tile done: lanes (c = 0, g = q) hold rows 4q .. 4q+3 of
-                // column 0; they go to the LDS output buffer (a global store
-                // here would lock its data registers until it completes, in
-                // order behind the weight loads in flight)
-                if (r == 0) {
-                    f32x4_t v;
-                    v.x = acc0.x + acc1.x;
-                    v.y = acc0.y + acc1.y;
-                    v.z = acc0.z + acc1.z;
-                    v.w = acc0.w + acc1.w;
-                    const int slot = CP.tile_begin + m.tile - T0;
-                    *reinterpret_cast<f32x4_t*>(ybuf + slot * 16 + 4 * q) = v;
+            const int beta = m.lc * kChunkBlocks + lane;  // block of this lane
+            const bool live = beta < CP.nblocks;
+            // row = beta / bpr: float estimate, corrected to the exact value
+            int row = (int)(((float)beta + 0.5f) * CP.inv_bpr);
+            row -= (row * CP.bpr > beta) ? 1 : 0;
+            row += ((row + 1) * CP.bpr <= beta) ? 1 : 0;
+            const int col = live ? beta - row * CP.bpr : 0;
+            // all 16 activation units of the block requested at once
+            const unsigned char* xb = xregion + CP.x_off + col * 16;
+            u32x4_t xv[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                xv[j] = *reinterpret_cast<const u32x4_t*>(xb + j * CP.bpr * 16);
+            }
+            // codebook byte planes (bf16-rounded entries); a block that is
+            // not live computes garbage on its own diagonal only
+            const uint32_t q0 = pack_bf16x2(__uint_as_float(r.c0.x), __uint_as_float(r.c0.y));
+            const uint32_t q1 = pack_bf16x2(__uint_as_float(r.c0.z), __uint_as_float(r.c0.w));
+            const uint32_t q2 = pack_bf16x2(__uint_as_float(r.c1.x), __uint_as_float(r.c1.y));
+            const uint32_t q3 = pack_bf16x2(__uint_as_float(r.c1.z), __uint_as_float(r.c1.w));
+            const uint32_t lo0 = __builtin_amdgcn_perm(q1, q0, 0x06040200u);
+            const uint32_t hi0 = __builtin_amdgcn_perm(q1, q0, 0x07050301u);
+            const uint32_t lo1 = __builtin_amdgcn_perm(q3, q2, 0x06040200u);
+            const uint32_t hi1 = __builtin_amdgcn_perm(q3, q2, 0x07050301u);
+            const uint32_t d[12] = {r.d0.x, r.d0.y, r.d0.z, r.d0.w, r.d1.x, r.d1.y,
+                                    r.d1.z, r.d1.w, r.d2.x, r.d2.y, r.d2.z, r.d2.w};
+            f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                uint32_t sel[8];
+                unit_selectors(d[3 * u], d[3 * u + 1], d[3 * u + 2], sel);
+#pragma unroll
+                for (int s = 0; s < 8; ++s) {
+                    const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sel[s]);
+                    const uint32_t ha = __builtin_amdgcn_perm(hi1, hi0, sel[s]);
+                    const uint32_t w0 = __builtin_amdgcn_perm(ha, la, 0x05010400u);
+                    const uint32_t w1 = __builtin_amdgcn_perm(ha, la, 0x07030602u);
+                    const u32x4_t& x = xv[4 * u + (s >> 1)];
+                    // two accumulators halve the dependent-MFMA chain
+                    if (s & 1) {
+                        acc1 = mfma44(w0, w1, x.z, x.w, acc1);
+                    } else {
+                        acc0 = mfma44(w0, w1, x.x, x.y, acc0);
+                    }
                 }
-                acc0 = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                acc1 = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+            // the lane's own dot product is diagonal element (lane & 3)
+            const f32x4_t a = acc0 + acc1;
+            const int l3 = lane & 3;
+            const float dot = l3 == 0 ? a.x : l3 == 1 ? a.y : l3 == 2 ? a.z : a.w;
+            // quad pre-sum where the quad's four blocks share a row
+            const int rowx = live ? row : -1 - lane;
+            const bool quad_row = quad_mov_i<quad_perm(0, 0, 0, 0)>(rowx) ==
+                                  quad_mov_i<quad_perm(3, 3, 3, 3)>(rowx);
+            const float s2 = dot + quad_mov<quad_perm(1, 0, 3, 2)>(dot);
+            const float s4 = s2 + quad_mov<quad_perm(2, 3, 0, 1)>(s2);
+            if (live && (!quad_row || l3 == 0)) {
+                const int part = (row * CP.bpr < m.lc * kChunkBlocks) ? 1 : 0;
+                atomicAdd(ybuf + CP.y_off + (row - CP.row_a) * 2 + part, quad_row ? s4 : dot);
             }
         };
 
-        // Three-register ring, unrolled so the sets rotate without copies:
-        // the loads of the two steps after the current one are in flight
-        // while it is consumed.  Validity is monotonic, so the first invalid
-        // set ends the wave's work.
-        Regs ra = {}, rb = {}, rc = {};
-        // (initialised: an undefined wave-uniform value is materialised with
-        // a v_readfirstlane of an arbitrary VGPR, which can be a load in
-        // flight)
-        Meta ma = {0, 0, 0, false}, mb = {0, 0, 0, false}, mc = {0, 0, 0, false};
-        const auto la = [](const uint8_t* p, const float* c, Regs& s) { set0::load_set(p, c, s); };
-        const auto lb = [](const uint8_t* p, const float* c, Regs& s) { set1::load_set(p, c, s); };
-        const auto lc = [](const uint8_t* p, const float* c, Regs& s) { set2::load_set(p, c, s); };
-        issue(la, ra, ma);
-        issue(lb, rb, mb);
-        while (true) {
-            issue(lc, rc, mc);
-            if (!ma.valid) break;
-            set0::wait_set(ra);
-            step(ra, ma);
-            issue(la, ra, ma);
-            if (!mb.valid) break;
-            set1::wait_set(rb);
-            step(rb, mb);
-            issue(lb, rb, mb);
-            if (!mc.valid) break;
-            set2::wait_set(rc);
-            step(rc, mc);
+        // Ring of kDepth slots, unrolled so each slot index is a constant.
+        // A slot is read into registers, refilled with the chunk kDepth
+        // ahead, and then computed, so kDepth chunks are in flight during
+        // the arithmetic.  Validity is monotonic: the first invalid slot
+        // ends the wave's work.  The loop issues no other vector-memory
+        // instruction, so the vmcnt waits count ring loads exactly.
+        constexpr int kAhead = (kDepth - 1) * kLoadsPerChunk;
+        Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
+        auto step = [&](int slot, Meta& m) {
+            wait_vm<kAhead>();
+            const SlotRegs r = read_slot(slot);
+            wait_lds();
+            const Meta cur = m;
+            issue(slot, m);
+            compute(r, cur);
+        };
+        issue(0, ma);
+        issue(1, mb);
+        if constexpr (kDepth == 2) {
+            while (true) {
+                if (!ma.valid) break;
+                step(0, ma);
+                if (!mb.valid) break;
+                step(1, mb);
+            }
+        } else {
+            issue(2, mc);
+            while (true) {
+                if (!ma.valid) break;
+                step(0, ma);
+                if (!mb.valid) break;
+                step(1, mb);
+                if (!mc.valid) break;
+                step(2, mc);
+            }
         }
-        wait_all(ra, rb, rc);
+        // the loads issued past the wave's last chunk land before the
+        // workgroup (and its LDS) can end
+        wait_vm<0>();
     }
 
     // ---- write the range's outputs (coalesced, after every wave is done) --
     __syncthreads();
     int li = 0;
-    for (int e = tid; e < (T1 - T0) * 16; e += 64 * kWaves) {
-        const int t = T0 + (e >> 4);
-        while (t >= pl[li].tile_begin + pl[li].tiles) ++li;
+    for (int e = tid; e < y_floats / 2; e += 64 * kWaves) {
+        while (e >= (pl[li].y_off >> 1) + (pl[li].row_b - pl[li].row_a)) ++li;
         const ProbL& P = pl[li];
-        const int row = (t - P.tile_begin) * 16 + (e & 15);
-        if (row < P.N) {
-            const float val = ybuf[e];
-            if (y_dtype == NB_BF16) {
-                *as_global_mut(static_cast<bf16_bits*>(P.y) + row) = f32_to_bf16_rne(val);
-            } else {
-                *as_global_mut(static_cast<float*>(P.y) + row) = val;
-            }
+        const int row = P.row_a + e - (P.y_off >> 1);
+        const float val = ybuf[2 * e] + ybuf[2 * e + 1];
+        if (y_dtype == NB_BF16) {
+            *as_global_mut(static_cast<bf16_bits*>(P.y) + row) = f32_to_bf16_rne(val);
+        } else {
+            *as_global_mut(static_cast<float*>(P.y) + row) = val;
         }
     }
 }
 
+// Chunks of one row-aligned tile of a problem: the smallest run of chunks
+// that starts and ends on row boundaries.
+int tile_chunks(int bpr) { return bpr / std::gcd(bpr, kChunkBlocks); }
+
 }  // namespace
 
-// LDS bytes the kernel uses for a range of tiles [a, b) over problems
+// LDS bytes the kernel uses for the chunk range [a, b) over problems
 // [pa, pb] (same layout as the kernel's set-up).
 static int64_t range_lds(const StreamProblem* hp, int pa, int pb, int a, int b) {
-    int64_t n = (int64_t)(pb - pa + 1) * (int64_t)sizeof(ProbL);
-    for (int p = pa; p <= pb; ++p) n += (int64_t)hp[p].K * 2;
-    return n + (int64_t)(b - a) * 16 * 4 + 16;
+    int64_t n = (int64_t)(pb - pa + 1) * (int64_t)sizeof(ProbL) +
+                (int64_t)kWaves * kDepth * kSlotBytes;
+    for (int p = pa; p <= pb; ++p) {
+        const StreamProblem& s = hp[p];
+        const int ca = std::max(a, s.chunk_begin) - s.chunk_begin;
+        const int cb = std::min(b, s.chunk_begin + s.nchunks) - s.chunk_begin;
+        const int64_t ra = ((int64_t)ca * kChunkBlocks) / s.bpr;
+        const int64_t rb = std::min<int64_t>(s.N, ((int64_t)cb * kChunkBlocks + s.bpr - 1) / s.bpr);
+        n += (int64_t)s.K * 2 + (rb - ra) * 2 * 4;
+    }
+    return n + 16;
 }
 
-// Problem holding tile t (host copy of the table; binary search).
-static int prob_of_tile(const StreamProblem* hp, int nprob, int t) {
+// Problem holding chunk c (host copy of the table; binary search).
+static int prob_of_chunk(const StreamProblem* hp, int nprob, int c) {
     int lo = 0, hi = nprob - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) / 2;
-        if (hp[mid].tile_begin <= t) lo = mid; else hi = mid - 1;
+        if (hp[mid].chunk_begin <= c) lo = mid; else hi = mid - 1;
     }
     return lo;
 }
 
-// First tile whose first step is at or after global step s.
-static int tile_at_step(const StreamProblem* hp, int nprob, int64_t s) {
-    int lo = 0, hi = nprob - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) / 2;
-        if (hp[mid].step_begin <= s) lo = mid; else hi = mid - 1;
-    }
-    const StreamProblem& P = hp[lo];
-    int64_t t = (s - P.step_begin + P.nsteps - 1) / P.nsteps;
-    if (t > P.tiles) t = P.tiles;
-    return P.tile_begin + (int)t;
+// The first row-aligned chunk boundary at or after global chunk c (a
+// problem's first and last chunk boundaries are row-aligned).
+static int aligned_at(const StreamProblem* hp, int nprob, int64_t c) {
+    const int p = prob_of_chunk(hp, nprob, (int)c);
+    const StreamProblem& P = hp[p];
+    const int64_t lc = c - P.chunk_begin;
+    const int64_t t = tile_chunks(P.bpr);
+    const int64_t up = std::min<int64_t>((lc + t - 1) / t * t, P.nchunks);
+    return P.chunk_begin + (int)up;
 }
 
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
                        int nprob, int y_dtype, hipStream_t stream) {
     if (nprob == 0) return NB_OK;
     const StreamProblem& last = host_probs[nprob - 1];
-    const int total_tiles = last.tile_begin + last.tiles;
-    const int64_t total_steps = (int64_t)last.step_begin + (int64_t)last.tiles * last.nsteps;
-    if (total_tiles == 0) return NB_OK;
+    const int total = last.chunk_begin + last.nchunks;
+    if (total == 0) return NB_OK;
     const int64_t lds_max = device_lds_bytes();
 
-    // Ranges balanced by steps, one per workgroup; a range whose problems,
-    // x vectors and outputs do not fit in LDS is halved (by steps) until
-    // they do.
-    const int64_t G = std::min<int64_t>((int64_t)device_cu_count() * NB_STREAM_WG_PER_CU,
-                                        total_tiles);
+    // Ranges balanced by chunks, one per workgroup, snapped forward to row
+    // boundaries; a range whose problems, x vectors and outputs do not fit
+    // in LDS is halved (at a row boundary) until they do.
+    const int64_t G = std::min<int64_t>((int64_t)device_cu_count() * NB_STREAM_WG_PER_CU, total);
     std::vector<int> bounds;
     bounds.reserve((size_t)G + 1);
-    for (int64_t g = 0; g <= G; ++g) bounds.push_back(tile_at_step(host_probs, nprob, g * total_steps / G));
+    bounds.push_back(0);
+    for (int64_t g = 1; g < G; ++g) {
+        const int b = aligned_at(host_probs, nprob, g * (int64_t)total / G);
+        if (b > bounds.back() && b < total) bounds.push_back(b);
+    }
+    bounds.push_back(total);
     std::vector<int> out;
-    out.push_back(bounds[0]);
-    for (int64_t g = 0; g < G; ++g) {
-        // split [bounds[g], bounds[g+1]) as needed (explicit stack)
-        std::vector<std::pair<int, int>> todo{{bounds[(size_t)g], bounds[(size_t)g + 1]}};
+    out.push_back(0);
+    for (size_t g = 0; g + 1 < bounds.size(); ++g) {
+        std::vector<std::pair<int, int>> todo{{bounds[g], bounds[g + 1]}};
         while (!todo.empty()) {
             auto [a, b] = todo.back();
             todo.pop_back();
             if (a >= b) continue;
-            const int pa = prob_of_tile(host_probs, nprob, a);
-            const int pb = prob_of_tile(host_probs, nprob, b - 1);
+            const int pa = prob_of_chunk(host_probs, nprob, a);
+            const int pb = prob_of_chunk(host_probs, nprob, b - 1);
             if (range_lds(host_probs, pa, pb, a, b) <= lds_max) {
                 out.push_back(b);
                 continue;
             }
-            if (b - a == 1) {
-                return fail(NB_EUNSUPPORTED, "nb_gemv_batched: one tile needs more LDS than %lld bytes",
+            const int mid = aligned_at(host_probs, nprob, a + (b - a) / 2);
+            if (mid <= a || mid >= b) {
+                return fail(NB_EUNSUPPORTED,
+                            "nb_gemv_batched: one row-aligned tile needs more LDS than %lld bytes",
                             (long long)lds_max);
             }
-            const int mid = a + (b - a) / 2;
             todo.push_back({mid, b});  // popped second
             todo.push_back({a, mid});
         }
@@ -513,11 +607,12 @@ int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host
         const int n = std::min(kStreamMaxGroups, nranges - c0);
         StreamRanges R;
         int64_t lds = 0;
-        for (int i = 0; i <= n; ++i) R.tile0[i] = out[(size_t)(c0 + i)];
+        for (int i = 0; i <= n; ++i) R.chunk0[i] = out[(size_t)(c0 + i)];
         for (int i = 0; i < n; ++i) {
-            R.prob0[i] = prob_of_tile(host_probs, nprob, R.tile0[i]);
-            R.prob1[i] = prob_of_tile(host_probs, nprob, R.tile0[i + 1] - 1);
-            lds = std::max(lds, range_lds(host_probs, R.prob0[i], R.prob1[i], R.tile0[i], R.tile0[i + 1]));
+            R.prob0[i] = prob_of_chunk(host_probs, nprob, R.chunk0[i]);
+            R.prob1[i] = prob_of_chunk(host_probs, nprob, R.chunk0[i + 1] - 1);
+            lds = std::max(lds, range_lds(host_probs, R.prob0[i], R.prob1[i], R.chunk0[i],
+                                          R.chunk0[i + 1]));
         }
         hipLaunchKernelGGL(gemv_stream_kernel, dim3(n), dim3(64 * kWaves), (size_t)lds, stream,
                            dev_probs, R, y_dtype);

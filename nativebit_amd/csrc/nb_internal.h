@@ -50,18 +50,17 @@ struct StreamProblem {
     void* y;                  // N outputs
     int32_t N, K;
     int32_t bpr;              // 128-weight blocks per row
-    int32_t nsteps;           // 512-column steps per row (ceil(bpr / 4))
-    int32_t tiles;            // 16-row tiles
-    int32_t tile_begin;       // first tile's index in the batch
-    int32_t step_begin;       // steps of all earlier problems (tiles * nsteps)
-    int32_t pad;
+    int32_t nchunks;          // 64-block chunks: ceil(N * bpr / 64)
+    int32_t chunk_begin;      // chunks of all earlier problems
+    int32_t pad[3];
 };
 
-// Tile ranges of one streaming launch (kernel argument, by value): workgroup
-// g owns tiles [tile0[g], tile0[g+1]) of problems prob0[g] .. prob1[g].
+// Chunk ranges of one streaming launch (kernel argument, by value):
+// workgroup g owns chunks [chunk0[g], chunk0[g+1]) of problems prob0[g] ..
+// prob1[g]; every range starts and ends on a row boundary.
 constexpr int kStreamMaxGroups = 256;
 struct StreamRanges {
-    int32_t tile0[kStreamMaxGroups + 1];
+    int32_t chunk0[kStreamMaxGroups + 1];
     int32_t prob0[kStreamMaxGroups];
     int32_t prob1[kStreamMaxGroups];
 };
