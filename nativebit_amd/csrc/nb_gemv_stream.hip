@@ -37,10 +37,12 @@
 // Row sums.  A row of bpr <= 64 blocks lies in at most two consecutive
 // chunks.  Lanes of a quad that share a row add their dot products in a
 // fixed order (DPP); the quad's sum, or each lane's own value where the
-// quad spans a row boundary, goes by LDS atomic to part[row][s], s = 0 in
-// the chunk where the row starts and 1 in the next.  Each slot receives the
-// lanes of one instruction of one wave, and y[row] = part[row][0] +
-// part[row][1], so results do not depend on which wave took which chunk.
+// quad spans a row boundary, goes by LDS atomic to sum[row] in the chunk
+// where the row starts, or to carry[chunk] for the blocks of a row that
+// began in the previous chunk.  Each slot receives the lanes of one
+// instruction of one wave, and y[row] = sum[row] + carry[the row's last
+// chunk] (when it differs from its first), so results do not depend on
+// which wave took which chunk.
 // Workgroup ranges start and end on row boundaries, so no row is shared
 // between workgroups; inside a workgroup waves take chunks one at a time
 // from a counter in LDS.
@@ -63,9 +65,11 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
 
-// waves per workgroup and chunks in flight per wave
+// waves per workgroup (three per SIMD: more waves hide the LDS and
+// memory waits of each other better than a deeper ring) and chunks in
+// flight per wave
 #ifndef NB_STREAM_WAVES
-#define NB_STREAM_WAVES 8
+#define NB_STREAM_WAVES 12
 #endif
 #ifndef NB_STREAM_DEPTH
 #define NB_STREAM_DEPTH 2
@@ -82,6 +86,13 @@ constexpr int kChunkIdxBytes = kChunkBlocks * 48;  // 3 KiB
 constexpr int kChunkCbBytes = kChunkBlocks * 32;   // 2 KiB
 constexpr int kSlotBytes = kChunkIdxBytes + kChunkCbBytes;
 constexpr int kLoadsPerChunk = 5;
+// LDS bytes of one column block's activations: 16 units of 16 bytes, padded
+// by one unit so that 16 consecutive blocks start in 16 different bank
+// groups (272 bytes = 68 banks apart)
+#ifndef NB_XCOL_UNITS
+#define NB_XCOL_UNITS 17
+#endif
+constexpr int kXColBytes = NB_XCOL_UNITS * 16;
 
 // Index offset o of selector s inside a 32-index unit: selector s yields
 // indices o, o+8, o+16, o+24 (see the file comment).
@@ -134,12 +145,13 @@ struct ProbL {
     const uint8_t* packed;
     const float* codebook;
     void* y;
-    int32_t N, bpr, nchunks, chunk_begin;
-    int32_t x_off;   // byte offset of this problem's x (permuted) in LDS
-    int32_t y_off;   // float offset of its (part0, part1) row pairs in LDS
-    int32_t row_a;   // first row of this problem in the range
-    int32_t row_b;   // one past the last row
-    int32_t pad[2];
+    int32_t nblocks, bpr, nchunks, chunk_begin;
+    int32_t x_off;      // byte offset of this problem's x (permuted) in LDS
+    int32_t y_off;      // float offset of its row sums (rows row_a..row_b-1)
+    int32_t row_a;      // first row of this problem in the range
+    int32_t row_b;      // one past the last row
+    int32_t carry_off;  // float offset of its carries (chunks ca..)
+    int32_t ca;         // first chunk of this problem in the range
 };
 static_assert(sizeof(ProbL) == 64, "ProbL is 64 bytes");
 
@@ -147,7 +159,7 @@ static_assert(sizeof(ProbL) == 64, "ProbL is 64 bytes");
 struct Prob {
     const uint8_t* packed;
     const float* codebook;
-    int nblocks, bpr, chunk_begin, chunk_end, x_off, y_off, row_a;
+    int nblocks, bpr, chunk_begin, chunk_end, x_off, y_off, row_a, carry_off, ca;
     float inv_bpr;
 };
 
@@ -163,14 +175,15 @@ __device__ __forceinline__ void read_prob(const ProbL* pl, int li, Prob& P) {
     const ProbL& s = pl[li];
     P.packed = uniform_ptr(s.packed);
     P.codebook = uniform_ptr(s.codebook);
-    const int N = __builtin_amdgcn_readfirstlane(s.N);
+    P.nblocks = __builtin_amdgcn_readfirstlane(s.nblocks);
     P.bpr = __builtin_amdgcn_readfirstlane(s.bpr);
-    P.nblocks = N * P.bpr;
     P.chunk_begin = __builtin_amdgcn_readfirstlane(s.chunk_begin);
     P.chunk_end = P.chunk_begin + __builtin_amdgcn_readfirstlane(s.nchunks);
     P.x_off = __builtin_amdgcn_readfirstlane(s.x_off);
     P.y_off = __builtin_amdgcn_readfirstlane(s.y_off);
     P.row_a = __builtin_amdgcn_readfirstlane(s.row_a);
+    P.carry_off = __builtin_amdgcn_readfirstlane(s.carry_off);
+    P.ca = __builtin_amdgcn_readfirstlane(s.ca);
     P.inv_bpr = 1.0f / (float)P.bpr;
 }
 
@@ -230,7 +243,8 @@ struct SlotRegs {
     u32x4_t d0, d1, d2, c0, c1;
 };
 
-__global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4)))
+void gemv_stream_kernel(
     const StreamProblem* __restrict__ probs, StreamRanges ranges, int y_dtype) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
@@ -259,7 +273,7 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
             d.packed = s.packed;
             d.codebook = s.codebook;
             d.y = s.y;
-            d.N = s.N;
+            d.nblocks = s.N * s.bpr;
             d.bpr = s.bpr;
             d.nchunks = s.nchunks;
             d.chunk_begin = s.chunk_begin;
@@ -267,18 +281,19 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
             d.y_off = y_floats;
             d.row_a = ra;
             d.row_b = rb;
-            d.pad[0] = d.pad[1] = 0;
+            d.carry_off = y_floats + (rb - ra);
+            d.ca = ca;
             pl[i] = d;
         }
-        x_bytes += s.K * 2;
-        y_floats += (rb - ra) * 2;
+        x_bytes += s.bpr * kXColBytes;
+        y_floats += (rb - ra) + (cb - ca);
     }
     float* ybuf = reinterpret_cast<float*>(xregion + x_bytes);
     int* next_chunk = reinterpret_cast<int*>(ybuf + y_floats);
     {
         // x of each problem in selector order: 16-byte unit j = 4u + m of
-        // column block c, at (j * bpr + c) * 16, holds the activations of
-        // selectors 2m and 2m+1 of unit u (4 bf16 each, in lookup order).
+        // column block c, at c * kXColBytes + j * 16, holds the activations
+        // of selectors 2m and 2m+1 of unit u (4 bf16 each, in lookup order).
         int off = 0;
         for (int i = 0; i < np; ++i) {
             const StreamProblem& s = probs[p0 + i];
@@ -303,10 +318,10 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
                     o.y = xs(oa + 16) | (xs(oa + 24) << 16);
                     o.z = xs(ob) | (xs(ob + 8) << 16);
                     o.w = xs(ob + 16) | (xs(ob + 24) << 16);
-                    *reinterpret_cast<u32x4_t*>(xregion + off + ((4 * u + m) * s.bpr + c) * 16) = o;
+                    *reinterpret_cast<u32x4_t*>(xregion + off + c * kXColBytes + (4 * u + m) * 16) = o;
                 }
             }
-            off += s.K * 2;
+            off += s.bpr * kXColBytes;
         }
     }
     for (int e = tid; e < y_floats; e += 64 * kWaves) ybuf[e] = 0.f;
@@ -334,10 +349,11 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
 
         // Loads the chunk at the load cursor into ring slot `slot` (always:
         // after the last chunk the cursor stays put and the load repeats),
-        // records where it belongs and moves the cursor to a new chunk.  In a
-        // problem's partial last chunk, lanes past the end of the stream
-        // re-read its last 16 bytes (their blocks are not live).
-        auto issue = [&](int slot, Meta& m) {
+        // records where it belongs and moves the cursor to chunk `next`
+        // (taken from the counter beforehand).  In a problem's partial last
+        // chunk, lanes past the end of the stream re-read its last 16 bytes
+        // (their blocks are not live).
+        auto issue = [&](int slot, Meta& m, int next) {
             const int lc = lchunk - LP.chunk_begin;
             const uint32_t dst = __builtin_amdgcn_readfirstlane(my_ring_lds + slot * kSlotBytes);
             const uint8_t* ip = LP.packed + (int64_t)lc * kChunkIdxBytes + 16 * lane;
@@ -363,13 +379,44 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
             m.lc = lc;
             m.valid = lvalid;
             if (!lvalid) return;
-            const int c = grab();
-            if (c >= C1) {
+            if (next >= C1) {
                 lvalid = false;  // repeat this chunk's addresses from now on
             } else {
-                lchunk = c;
+                lchunk = next;
                 while (lchunk >= LP.chunk_end) read_prob(pl, ++li, LP);
             }
+        };
+
+        int ci = -1;  // problem whose fields are in CP
+        Prob CP = {};
+
+        // Per-chunk lane state computed before the chunk's bytes arrive.
+        struct Lane {
+            int row;
+            bool live;
+        };
+        // The lane's block, row and column; requests its 16 activation
+        // units from LDS.
+        auto prepare = [&](const Meta& m, u32x4_t (&xv)[16]) -> Lane {
+            if (m.li != ci) {
+                read_prob(pl, m.li, CP);
+                ci = m.li;
+            }
+            const int beta = m.lc * kChunkBlocks + lane;  // block of this lane
+            Lane L;
+            L.live = beta < CP.nblocks;
+            // row = beta / bpr (beta < 2^24): float estimate, off by at most
+            // one, then corrected
+            int row = (int)__builtin_fmaf((float)beta, CP.inv_bpr, 0.5f * CP.inv_bpr);
+            int rem = beta - (int)__umul24((unsigned)row, (unsigned)CP.bpr);
+            row += rem >= CP.bpr ? 1 : (rem < 0 ? -1 : 0);
+            rem = beta - (int)__umul24((unsigned)row, (unsigned)CP.bpr);
+            L.row = row;
+            const int col = L.live ? rem : 0;
+            const unsigned char* xb = xregion + CP.x_off + col * kXColBytes;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
+            return L;
         };
 
         // This lane's 48 index bytes and 32 codebook bytes of a slot, in
@@ -387,28 +434,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
             return r;
         };
 
-        int ci = -1;  // problem whose fields are in CP
-        Prob CP = {};
-
-        auto compute = [&](const SlotRegs& r, const Meta& m) {
-            if (m.li != ci) {
-                read_prob(pl, m.li, CP);
-                ci = m.li;
-            }
-            const int beta = m.lc * kChunkBlocks + lane;  // block of this lane
-            const bool live = beta < CP.nblocks;
-            // row = beta / bpr: float estimate, corrected to the exact value
-            int row = (int)(((float)beta + 0.5f) * CP.inv_bpr);
-            row -= (row * CP.bpr > beta) ? 1 : 0;
-            row += ((row + 1) * CP.bpr <= beta) ? 1 : 0;
-            const int col = live ? beta - row * CP.bpr : 0;
-            // all 16 activation units of the block requested at once
-            const unsigned char* xb = xregion + CP.x_off + col * 16;
-            u32x4_t xv[16];
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                xv[j] = *reinterpret_cast<const u32x4_t*>(xb + j * CP.bpr * 16);
-            }
+        auto compute = [&](const SlotRegs& r, const Meta& m, const Lane& L,
+                           const u32x4_t (&xv)[16]) {
             // codebook byte planes (bf16-rounded entries); a block that is
             // not live computes garbage on its own diagonal only
             const uint32_t q0 = pack_bf16x2(__uint_as_float(r.c0.x), __uint_as_float(r.c0.y));
@@ -446,36 +473,44 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
             const int l3 = lane & 3;
             const float dot = l3 == 0 ? a.x : l3 == 1 ? a.y : l3 == 2 ? a.z : a.w;
             // quad pre-sum where the quad's four blocks share a row
-            const int rowx = live ? row : -1 - lane;
+            const int rowx = L.live ? L.row : -1 - lane;
             const bool quad_row = quad_mov_i<quad_perm(0, 0, 0, 0)>(rowx) ==
                                   quad_mov_i<quad_perm(3, 3, 3, 3)>(rowx);
             const float s2 = dot + quad_mov<quad_perm(1, 0, 3, 2)>(dot);
             const float s4 = s2 + quad_mov<quad_perm(2, 3, 0, 1)>(s2);
-            if (live && (!quad_row || l3 == 0)) {
-                const int part = (row * CP.bpr < m.lc * kChunkBlocks) ? 1 : 0;
-                atomicAdd(ybuf + CP.y_off + (row - CP.row_a) * 2 + part, quad_row ? s4 : dot);
+            if (L.live && (!quad_row || l3 == 0)) {
+                // a row that began in the previous chunk goes to this
+                // chunk's carry slot
+                const bool carry = L.row * CP.bpr < m.lc * kChunkBlocks;
+                const int slot = carry ? CP.carry_off + m.lc - CP.ca : CP.y_off + L.row - CP.row_a;
+                atomicAdd(ybuf + slot, quad_row ? s4 : dot);
             }
         };
 
         // Ring of kDepth slots, unrolled so each slot index is a constant.
-        // A slot is read into registers, refilled with the chunk kDepth
-        // ahead, and then computed, so kDepth chunks are in flight during
-        // the arithmetic.  Validity is monotonic: the first invalid slot
-        // ends the wave's work.  The loop issues no other vector-memory
+        // One step: take the next chunk number from the counter and request
+        // this chunk's activations (both LDS, in flight while the wave waits
+        // for the chunk), read the slot into registers, refill it with the
+        // chunk kDepth ahead, and compute -- kDepth chunks are in flight
+        // during the arithmetic.  Validity is monotonic: the first invalid
+        // slot ends the wave's work.  The loop issues no other vector-memory
         // instruction, so the vmcnt waits count ring loads exactly.
         constexpr int kAhead = (kDepth - 1) * kLoadsPerChunk;
         Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
         auto step = [&](int slot, Meta& m) {
+            const int next = lvalid ? grab() : C1;
+            u32x4_t xv[16];
+            const Lane L = prepare(m, xv);
             wait_vm<kAhead>();
             const SlotRegs r = read_slot(slot);
             wait_lds();
             const Meta cur = m;
-            issue(slot, m);
-            compute(r, cur);
+            issue(slot, m, next);
+            compute(r, cur, L, xv);
         };
-        issue(0, ma);
-        issue(1, mb);
+        issue(0, ma, grab());
         if constexpr (kDepth == 2) {
+            issue(1, mb, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
                 step(0, ma);
@@ -483,7 +518,8 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
                 step(1, mb);
             }
         } else {
-            issue(2, mc);
+            issue(1, mb, lvalid ? grab() : C1);
+            issue(2, mc, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
                 step(0, ma);
@@ -500,16 +536,20 @@ __global__ __launch_bounds__(64 * kWaves) void gemv_stream_kernel(
 
     // ---- write the range's outputs (coalesced, after every wave is done) --
     __syncthreads();
-    int li = 0;
-    for (int e = tid; e < y_floats / 2; e += 64 * kWaves) {
-        while (e >= (pl[li].y_off >> 1) + (pl[li].row_b - pl[li].row_a)) ++li;
-        const ProbL& P = pl[li];
-        const int row = P.row_a + e - (P.y_off >> 1);
-        const float val = ybuf[2 * e] + ybuf[2 * e + 1];
-        if (y_dtype == NB_BF16) {
-            *as_global_mut(static_cast<bf16_bits*>(P.y) + row) = f32_to_bf16_rne(val);
-        } else {
-            *as_global_mut(static_cast<float*>(P.y) + row) = val;
+    for (int i = 0; i < np; ++i) {
+        const ProbL& P = pl[i];
+        for (int e = tid; e < P.row_b - P.row_a; e += 64 * kWaves) {
+            const int row = P.row_a + e;
+            float val = ybuf[P.y_off + e];
+            // the row's tail, if its last block lies in a later chunk
+            const int c_first = (row * P.bpr) / kChunkBlocks;
+            const int c_last = (row * P.bpr + P.bpr - 1) / kChunkBlocks;
+            if (c_last != c_first) val += ybuf[P.carry_off + c_last - P.ca];
+            if (y_dtype == NB_BF16) {
+                *as_global_mut(static_cast<bf16_bits*>(P.y) + row) = f32_to_bf16_rne(val);
+            } else {
+                *as_global_mut(static_cast<float*>(P.y) + row) = val;
+            }
         }
     }
 }
@@ -531,7 +571,7 @@ static int64_t range_lds(const StreamProblem* hp, int pa, int pb, int a, int b) 
         const int cb = std::min(b, s.chunk_begin + s.nchunks) - s.chunk_begin;
         const int64_t ra = ((int64_t)ca * kChunkBlocks) / s.bpr;
         const int64_t rb = std::min<int64_t>(s.N, ((int64_t)cb * kChunkBlocks + s.bpr - 1) / s.bpr);
-        n += (int64_t)s.K * 2 + (rb - ra) * 2 * 4;
+        n += (int64_t)s.bpr * kXColBytes + ((rb - ra) + (cb - ca)) * 4;
     }
     return n + 16;
 }
@@ -565,42 +605,48 @@ int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host
     if (total == 0) return NB_OK;
     const int64_t lds_max = device_lds_bytes();
 
-    // Ranges balanced by chunks, one per workgroup, snapped forward to row
-    // boundaries; a range whose problems, x vectors and outputs do not fit
-    // in LDS is halved (at a row boundary) until they do.
+    // Ranges balanced by chunks, one per workgroup: each takes an equal
+    // share of the chunks still unassigned, snapped forward to a row
+    // boundary.  A range whose problems, x vectors and outputs do not fit in
+    // LDS first ends early, at the start of its last problem (the later
+    // ranges share the piece); failing that it is halved (at a row
+    // boundary) until it fits.
     const int64_t G = std::min<int64_t>((int64_t)device_cu_count() * NB_STREAM_WG_PER_CU, total);
-    std::vector<int> bounds;
-    bounds.reserve((size_t)G + 1);
-    bounds.push_back(0);
-    for (int64_t g = 1; g < G; ++g) {
-        const int b = aligned_at(host_probs, nprob, g * (int64_t)total / G);
-        if (b > bounds.back() && b < total) bounds.push_back(b);
-    }
-    bounds.push_back(total);
+    auto fits = [&](int a, int b) {
+        return range_lds(host_probs, prob_of_chunk(host_probs, nprob, a),
+                         prob_of_chunk(host_probs, nprob, b - 1), a, b) <= lds_max;
+    };
     std::vector<int> out;
+    out.reserve((size_t)G + 8);
     out.push_back(0);
-    for (size_t g = 0; g + 1 < bounds.size(); ++g) {
-        std::vector<std::pair<int, int>> todo{{bounds[g], bounds[g + 1]}};
+    for (int64_t g = 1; g <= G; ++g) {
+        const int a = out.back();
+        int b = g == G ? total : aligned_at(host_probs, nprob, a + (total - a) / (G - g + 1));
+        if (b <= a) continue;
+        if (!fits(a, b)) {
+            const int pl = host_probs[prob_of_chunk(host_probs, nprob, b - 1)].chunk_begin;
+            if (pl > a && fits(a, pl)) b = pl;
+        }
+        std::vector<std::pair<int, int>> todo{{a, b}};
         while (!todo.empty()) {
-            auto [a, b] = todo.back();
+            auto [x0, x1] = todo.back();
             todo.pop_back();
-            if (a >= b) continue;
-            const int pa = prob_of_chunk(host_probs, nprob, a);
-            const int pb = prob_of_chunk(host_probs, nprob, b - 1);
-            if (range_lds(host_probs, pa, pb, a, b) <= lds_max) {
-                out.push_back(b);
+            if (x0 >= x1) continue;
+            if (fits(x0, x1)) {
+                out.push_back(x1);
                 continue;
             }
-            const int mid = aligned_at(host_probs, nprob, a + (b - a) / 2);
-            if (mid <= a || mid >= b) {
+            const int mid = aligned_at(host_probs, nprob, x0 + (x1 - x0) / 2);
+            if (mid <= x0 || mid >= x1) {
                 return fail(NB_EUNSUPPORTED,
                             "nb_gemv_batched: one row-aligned tile needs more LDS than %lld bytes",
                             (long long)lds_max);
             }
-            todo.push_back({mid, b});  // popped second
-            todo.push_back({a, mid});
+            todo.push_back({mid, x1});  // popped second
+            todo.push_back({x0, mid});
         }
     }
+    if (out.back() != total) out.push_back(total);  // (never: the last range ends at total)
     // launch in chunks of at most kStreamMaxGroups workgroups
     const int nranges = (int)out.size() - 1;
     for (int c0 = 0; c0 < nranges; c0 += kStreamMaxGroups) {
