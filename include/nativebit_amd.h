@@ -164,6 +164,77 @@ int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
 int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count,
                     int y_dtype, void* stream);
 
+
+/* ------------------------------------------------------------------------
+ * Decode step (one token, batch 1) -- the non-GEMV kernels of the packed
+ * decoder of inference/generate_torch.py, for callers that run the whole
+ * step on the device (for instance captured once in a HIP graph).  The
+ * current position and token live in device memory (nb_decode_state), so no
+ * step needs a host round trip.  All functions enqueue on `stream`.
+ * ------------------------------------------------------------------------ */
+typedef struct nb_decode_state {
+    uint64_t key;    /* argmax key of the step in progress (0 between steps) */
+    int32_t pos;     /* position of the token being fed                     */
+    int32_t token;   /* token being fed                                     */
+    int32_t step;    /* index of the next entry of tokens_out               */
+    uint32_t done;   /* workgroup counter of nb_lm_head_argmax (0 between)  */
+} nb_decode_state;
+
+/*
+ * x (+)= y, then h = (x / sqrt(mean(x^2) + eps)) * w  (n elements; x, y, w
+ * fp32, h NB_F32 or NB_BF16).  With emb != NULL the row emb[state->token]
+ * (fp32, n wide) replaces x first (the embedding lookup); with y != NULL
+ * (and emb == NULL) y is added to x first (the residual).  x is updated in
+ * place.
+ * Replaces: RMSNorm.forward (inference/generate_torch.py:29-38) with the
+ *           residual adds of TransformerBlock.forward (128-132) and the
+ *           embedding lookup of PackedGPT.forward (150).
+ */
+int nb_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* state,
+                   const float* w, void* h, int h_dtype, int n, float eps, void* stream);
+
+/*
+ * One token of causal self-attention for all heads at position state->pos:
+ * RoPE of the query and key (pairs (2i, 2i+1), angle pos * theta^(-2i/D),
+ * tables cos/sin of [ctx][D/2] fp32), append of the rotated key and the
+ * value to the caches ([n_head][ctx][D] fp32 each), softmax(q k^T / sqrt(D))
+ * over positions 0..pos, output [n_head * D] (NB_F32 or NB_BF16).  A
+ * position outside 0..ctx-1 leaves caches and output untouched.
+ * qkv: [3 * n_head * D] fp32, q | k | v.  work: nb_attention_work_floats()
+ * floats; done: n_head uint32 counters, zero before the first call (each
+ * call leaves them zero).
+ * Replaces: CausalAttention.forward for one token with a KV cache, minus
+ *           the two projections (inference/generate_torch.py:48-60, 72-106).
+ */
+int nb_attention_step(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                      const float* sin_t, const nb_decode_state* state, float* work,
+                      uint32_t* done, void* out, int out_dtype, int n_head, int head_dim,
+                      int ctx, void* stream);
+int nb_attention_work_floats(int n_head);
+
+/*
+ * act[i] = silu(gu[i]) * gu[n + i]  (gu fp32 gate | up, act NB_F32/NB_BF16).
+ * Replaces: F.silu(gate(x)) * up(x) (inference/generate_torch.py:116-117).
+ */
+int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream);
+
+/*
+ * Tied LM head with soft cap and greedy choice: l[v] = 30 tanh((h . emb[v])
+ * / 30) for v < V (h bf16 [C], emb bf16 [V][C], C % 8 == 0); logits (if not
+ * NULL) receives l; the first v with the largest l is written to
+ * tokens_out[state->step] (when state->step < tokens_cap) and becomes
+ * state->token -- unless
+ * state->step < n_force, in which case force[state->step] becomes the next
+ * token (teacher forcing, to feed a prompt) -- and state->pos and
+ * state->step advance by one.  state->key and state->done must be zero
+ * before the call (every call leaves them zero).
+ * Replaces: the head and argmax of PackedGPT.forward / benchmark
+ *           (inference/generate_torch.py:157-159, 311).
+ */
+int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* state,
+                      int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
+                      int V, int C, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

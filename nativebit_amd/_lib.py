@@ -50,6 +50,11 @@ SIGNATURES = {
     "nb_gemv_batch_table_bytes": (_L, [_I]),
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),
+    "nb_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P]),
+    "nb_attention_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "nb_attention_work_floats": (_I, [_I]),
+    "nb_silu_mul": (_I, [_P, _P, _I, _I, _P]),
+    "nb_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
 }
 
 
@@ -58,6 +63,12 @@ class BatchItem(ctypes.Structure):
     _fields_ = [("x", ctypes.c_void_p), ("packed", ctypes.c_void_p),
                 ("codebook", ctypes.c_void_p), ("y", ctypes.c_void_p),
                 ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
+
+
+class DecodeState(ctypes.Structure):
+    """struct nb_decode_state (include/nativebit_amd.h)."""
+    _fields_ = [("key", ctypes.c_uint64), ("pos", ctypes.c_int32), ("token", ctypes.c_int32),
+                ("step", ctypes.c_int32), ("done", ctypes.c_uint32)]
 
 
 class NativeBitError(RuntimeError):

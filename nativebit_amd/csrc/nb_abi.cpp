@@ -322,3 +322,84 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
 }
 
 }  // extern "C"
+
+extern "C" {
+
+int nb_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* state,
+                   const float* w, void* h, int h_dtype, int n, float eps, void* stream) {
+    const char* fn = "nb_add_rmsnorm";
+    if (n < 1) return fail(NB_EINVAL, "%s: n=%d < 1", fn, n);
+    if (!x || !w || !h) return fail(NB_EINVAL, "%s: NULL x/w/h", fn);
+    if (emb && !state) return fail(NB_EINVAL, "%s: emb given without a state", fn);
+    if (h_dtype != NB_F32 && h_dtype != NB_BF16) return fail(NB_EINVAL, "%s: h_dtype=%d", fn, h_dtype);
+    if (!(eps >= 0.f)) return fail(NB_EINVAL, "%s: eps must be >= 0", fn);
+    if (!aligned(x, 4) || !aligned(w, 4) || (y && !aligned(y, 4)) || (emb && !aligned(emb, 4)) ||
+        !aligned(h, dtype_size(h_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    int st = ensure_device();
+    if (st) return st;
+    return launch_add_rmsnorm(x, y, emb, state, w, h, h_dtype, n, eps, static_cast<hipStream_t>(stream));
+}
+
+int nb_attention_work_floats(int n_head) { return n_head > 0 ? attention_work_floats(n_head) : 0; }
+
+int nb_attention_step(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                      const float* sin_t, const nb_decode_state* state, float* work,
+                      uint32_t* done, void* out, int out_dtype, int n_head, int head_dim,
+                      int ctx, void* stream) {
+    const char* fn = "nb_attention_step";
+    if (n_head < 1 || ctx < 1) return fail(NB_EINVAL, "%s: n_head=%d ctx=%d", fn, n_head, ctx);
+    if (head_dim < 2 || head_dim % 2 || head_dim > attention_max_head_dim()) {
+        return fail(NB_EUNSUPPORTED, "%s: head_dim=%d (even, <= %d)", fn, head_dim,
+                    attention_max_head_dim());
+    }
+    if (!qkv || !k_cache || !v_cache || !cos_t || !sin_t || !state || !work || !done || !out) {
+        return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    }
+    if (out_dtype != NB_F32 && out_dtype != NB_BF16) return fail(NB_EINVAL, "%s: out_dtype=%d", fn, out_dtype);
+    if (!aligned(qkv, 4) || !aligned(k_cache, 4) || !aligned(v_cache, 4) || !aligned(work, 4) ||
+        !aligned(done, 4) || !aligned(out, dtype_size(out_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    int st = ensure_device();
+    if (st) return st;
+    return launch_attention_step(qkv, k_cache, v_cache, cos_t, sin_t, state, work, done, out,
+                                 out_dtype, n_head, head_dim, ctx, static_cast<hipStream_t>(stream));
+}
+
+int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream) {
+    const char* fn = "nb_silu_mul";
+    if (n < 1) return fail(NB_EINVAL, "%s: n=%d < 1", fn, n);
+    if (!gu || !act) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (act_dtype != NB_F32 && act_dtype != NB_BF16) return fail(NB_EINVAL, "%s: act_dtype=%d", fn, act_dtype);
+    if (!aligned(gu, 4) || !aligned(act, dtype_size(act_dtype))) return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    int st = ensure_device();
+    if (st) return st;
+    return launch_silu_mul(gu, act, act_dtype, n, static_cast<hipStream_t>(stream));
+}
+
+int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* state,
+                      int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
+                      int V, int C, void* stream) {
+    const char* fn = "nb_lm_head_argmax";
+    if (V < 1 || C < 8 || C % 8 || C > lm_head_max_c()) {
+        return fail(NB_EUNSUPPORTED, "%s: V=%d C=%d (C %% 8 == 0, 8 <= C <= %d)", fn, V, C,
+                    lm_head_max_c());
+    }
+    if (!h || !emb || !state) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (n_force < 0 || (n_force > 0 && !force)) return fail(NB_EINVAL, "%s: n_force=%d without force", fn, n_force);
+    if (tokens_cap < 0 || (tokens_cap > 0 && !tokens_out)) {
+        return fail(NB_EINVAL, "%s: tokens_cap=%d without tokens_out", fn, tokens_cap);
+    }
+    if (!aligned(h, 2) || !aligned(emb, 16) || (logits && !aligned(logits, 4)) ||
+        !aligned(state, 8) || (tokens_out && !aligned(tokens_out, 4))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    int st = ensure_device();
+    if (st) return st;
+    return launch_lm_head_argmax(h, emb, logits, state, tokens_out, tokens_cap, force, n_force,
+                                 V, C, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

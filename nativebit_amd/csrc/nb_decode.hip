@@ -1,0 +1,344 @@
+// Kernels of one greedy decode step of the packed NativeBit decoder (gfx950),
+// everything but the packed GEMVs:
+//
+//   nb_add_rmsnorm      x (+)= y (or x = embedding[token]); h = rmsnorm(x) * w
+//                       (generate_torch.py:29-38, residuals 128-132, 150)
+//   nb_attention_step   RoPE at the current position, K/V append, softmax
+//                       attention over positions 0..pos for every head
+//                       (generate_torch.py:48-60, 72-106 with T = 1)
+//   nb_silu_mul         silu(gate) * up (generate_torch.py:116-117)
+//   nb_lm_head_argmax   tied head, 30 tanh(l / 30) soft cap, greedy argmax,
+//                       position advance (generate_torch.py:157-159, 311)
+//
+// The position and the current token live in a device-side nb_decode_state,
+// so a whole step is a fixed sequence of launches that can be captured once
+// in a HIP graph and replayed per token without a host round trip.
+// Arithmetic is fp32 (activations may be handed on as bf16, rounded to
+// nearest even).
+#include <math.h>
+
+#include <algorithm>
+
+#include "nb_device.h"
+#include "nb_internal.h"
+
+namespace nb {
+namespace {
+
+__device__ __forceinline__ float load_act(const void* p, int dtype, int64_t i) {
+    if (dtype == NB_BF16) return bf16_to_f32(static_cast<const bf16_bits*>(p)[i]);
+    return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_act(void* p, int dtype, int64_t i, float v) {
+    if (dtype == NB_BF16) {
+        static_cast<bf16_bits*>(p)[i] = f32_to_bf16_rne(v);
+    } else {
+        static_cast<float*>(p)[i] = v;
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum of one value per thread (blockDim.x a multiple of 64,
+// at most 1024).
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int w = 0; w < nw; ++w) t += red[w];  // same order in every thread
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm with the residual add or the embedding lookup in front
+// ---------------------------------------------------------------------------
+constexpr int kNormThreads = 1024;
+
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
+    float* __restrict__ x, const float* __restrict__ y, const float* __restrict__ emb,
+    const nb_decode_state* __restrict__ st, const float* __restrict__ w, void* __restrict__ h,
+    int h_dtype, int n, float eps) {
+    __shared__ float red[kNormThreads / 64];
+    const float* src_row = nullptr;
+    if (emb) src_row = emb + (int64_t)st->token * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        float v;
+        if (src_row) {
+            v = src_row[i];
+        } else {
+            v = x[i];
+            if (y) v = v + y[i];
+        }
+        if (src_row || y) x[i] = v;
+        ss += v * v;
+    }
+    const float mean = block_sum(ss, red) / (float)n;
+    const float norm = sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        // (x / norm) * w, as generate_torch.py:37
+        store_act(h, h_dtype, i, (x[i] / norm) * w[i]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// attention for one new token, split over positions
+// ---------------------------------------------------------------------------
+// Grid (n_head, kAttnSplits); block 256 threads = 4 waves.  Workgroup
+// (hd, s) takes positions s, s + S, s + 2S, ... <= pos; each wave takes one
+// position at a time, its 64 lanes covering head_dim in pairs.  Partial
+// softmax state (max, sum, weighted V) goes to the workspace; the last
+// workgroup of a head (atomic counter) combines the splits in split order.
+// Every workgroup rotates the new query and key itself and uses the new
+// key/value directly at t == pos, so only workgroup (hd, 0) writes the cache
+// and nothing reads what another workgroup writes in the same launch.
+constexpr int kAttnSplits = 16;
+constexpr int kAttnThreads = 256;
+constexpr int kMaxHeadDim = 256;
+
+__global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
+    const float* __restrict__ qkv, float* __restrict__ k_cache, float* __restrict__ v_cache,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const nb_decode_state* __restrict__ st, float* __restrict__ work, unsigned* __restrict__ done,
+    void* __restrict__ out, int out_dtype, int n_head, int D, int ctx) {
+    __shared__ float q[kMaxHeadDim], kn[kMaxHeadDim], vn[kMaxHeadDim];
+    __shared__ float wm[kAttnThreads / 64], wl[kAttnThreads / 64];
+    __shared__ float wo[kAttnThreads / 64][kMaxHeadDim];
+    __shared__ unsigned last;
+    const int hd = blockIdx.x, s = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = st->pos;
+    if (pos < 0 || pos >= ctx) return;  // past the cache: nothing to do
+    const int C = n_head * D;
+    const float scale = 1.0f / sqrtf((float)D);
+    // RoPE of the new query and key (pairs (2i, 2i+1) rotated by angle i)
+    for (int i = tid; i < D / 2; i += kAttnThreads) {
+        const float c = cos_t[(int64_t)pos * (D / 2) + i], sn = sin_t[(int64_t)pos * (D / 2) + i];
+        const float q0 = qkv[hd * D + 2 * i], q1 = qkv[hd * D + 2 * i + 1];
+        const float k0 = qkv[C + hd * D + 2 * i], k1 = qkv[C + hd * D + 2 * i + 1];
+        // q * cos2 + rotate(q) * sin2, then the reference's (q * scale)
+        q[2 * i] = __fmul_rn(__fadd_rn(__fmul_rn(q0, c), __fmul_rn(-q1, sn)), scale);
+        q[2 * i + 1] = __fmul_rn(__fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, sn)), scale);
+        kn[2 * i] = __fadd_rn(__fmul_rn(k0, c), __fmul_rn(-k1, sn));
+        kn[2 * i + 1] = __fadd_rn(__fmul_rn(k1, c), __fmul_rn(k0, sn));
+    }
+    for (int d = tid; d < D; d += kAttnThreads) vn[d] = qkv[2 * C + hd * D + d];
+    __syncthreads();
+    if (s == 0) {
+        for (int d = tid; d < D; d += kAttnThreads) {
+            k_cache[((int64_t)hd * ctx + pos) * D + d] = kn[d];
+            v_cache[((int64_t)hd * ctx + pos) * D + d] = vn[d];
+        }
+    }
+    // this wave's positions: t = s + S * (wave + 4 j)
+    float m = -INFINITY, l = 0.f;
+    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;  // dims lane, lane+64, +128, +192
+    const float* kc = k_cache + (int64_t)hd * ctx * D;
+    const float* vc = v_cache + (int64_t)hd * ctx * D;
+    for (int t = s + kAttnSplits * wave; t <= pos; t += kAttnSplits * (kAttnThreads / 64)) {
+        const float* kr = t == pos ? kn : kc + (int64_t)t * D;
+        const float* vr = t == pos ? vn : vc + (int64_t)t * D;
+        float part = 0.f;
+        for (int d = lane; d < D; d += 64) part += q[d] * kr[d];
+        const float sc = wave_sum(part);
+        const float mn = fmaxf(m, sc);
+        const float a = __expf(m - mn), b = __expf(sc - mn);
+        l = l * a + b;
+        if (lane < D) o0 = o0 * a + b * vr[lane];
+        if (lane + 64 < D) o1 = o1 * a + b * vr[lane + 64];
+        if (lane + 128 < D) o2 = o2 * a + b * vr[lane + 128];
+        if (lane + 192 < D) o3 = o3 * a + b * vr[lane + 192];
+        m = mn;
+    }
+    // combine the 4 waves of this workgroup
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
+    wo[wave][lane] = o0;
+    wo[wave][lane + 64] = o1;
+    wo[wave][lane + 128] = o2;
+    wo[wave][lane + 192] = o3;
+    __syncthreads();
+    float* wk = work + ((int64_t)hd * kAttnSplits + s) * (kMaxHeadDim + 2);
+    if (tid < D) {
+        float M = -INFINITY;
+        for (int w = 0; w < kAttnThreads / 64; ++w) M = fmaxf(M, wm[w]);
+        float L = 0.f, O = 0.f;
+        for (int w = 0; w < kAttnThreads / 64; ++w) {
+            const float f = wm[w] == -INFINITY ? 0.f : __expf(wm[w] - M);
+            L += f * wl[w];
+            O += f * wo[w][tid];
+        }
+        wk[2 + tid] = O;
+        if (tid == 0) {
+            wk[0] = M;
+            wk[1] = L;
+        }
+    }
+    // the last workgroup of this head combines the splits
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(done + hd, 1u) == kAttnSplits - 1 ? 1u : 0u;
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    if (tid < D) {
+        const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
+        float M = -INFINITY;
+        for (int j = 0; j < kAttnSplits; ++j) M = fmaxf(M, __builtin_nontemporal_load(base + j * (kMaxHeadDim + 2)));
+        float L = 0.f, O = 0.f;
+        for (int j = 0; j < kAttnSplits; ++j) {
+            const float* p = base + j * (kMaxHeadDim + 2);
+            const float mj = __builtin_nontemporal_load(p);
+            const float f = mj == -INFINITY ? 0.f : __expf(mj - M);
+            L += f * __builtin_nontemporal_load(p + 1);
+            O += f * __builtin_nontemporal_load(p + 2 + tid);
+        }
+        store_act(out, out_dtype, hd * D + tid, O / L);
+    }
+    if (tid == 0) done[hd] = 0u;  // ready for the next step
+}
+
+// ---------------------------------------------------------------------------
+// silu(gate) * up
+// ---------------------------------------------------------------------------
+__global__ void silu_mul_kernel(const float* __restrict__ gu, void* __restrict__ act, int dtype,
+                                int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        const float g = gu[i];
+        const float sg = g / (1.0f + expf(-g));
+        store_act(act, dtype, i, sg * gu[n + i]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// tied LM head, soft cap, greedy argmax, position advance
+// ---------------------------------------------------------------------------
+// One wave per row at a time: each lane holds 8 * (C / 512) of h's values as
+// fp32 and reads the row's bf16 in 16-byte pieces.  The argmax key is
+// (order-preserving bits of the capped logit) << 32 | (0xffffffff - row),
+// so the largest key is the first row with the largest value -- torch's
+// argmax -- whatever the order of the atomics.  The last workgroup to
+// finish (atomic counter) turns the key into the next token.
+constexpr int kHeadThreads = 256;
+constexpr int kHeadMaxC = 8192;
+
+__device__ __forceinline__ uint32_t orderable(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
+    const bf16_bits* __restrict__ h, const bf16_bits* __restrict__ emb, float* __restrict__ logits,
+    nb_decode_state* __restrict__ st, int32_t* __restrict__ tokens_out, int tokens_cap,
+    const int32_t* __restrict__ force, int n_force, int V, int C) {
+    __shared__ float hs[kHeadMaxC];
+    __shared__ unsigned long long wkey[kHeadThreads / 64];
+    __shared__ unsigned last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int i = tid; i < C; i += kHeadThreads) hs[i] = bf16_to_f32(h[i]);
+    __syncthreads();
+    unsigned long long best = 0ull;
+    const int nwaves = gridDim.x * (kHeadThreads / 64);
+    for (int r = blockIdx.x * (kHeadThreads / 64) + wave; r < V; r += nwaves) {
+        const bf16_bits* row = emb + (int64_t)r * C;
+        float acc = 0.f;
+        for (int c = lane * 8; c < C; c += 512) {
+            typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(row + c));
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc += hs[c + 2 * j] * __uint_as_float(wv[j] << 16);
+                acc += hs[c + 2 * j + 1] * __uint_as_float(wv[j] & 0xffff0000u);
+            }
+        }
+        acc = wave_sum(acc);
+        const float capped = 30.0f * tanhf(acc / 30.0f);
+        if (lane == 0) {
+            if (logits) logits[r] = capped;
+            const unsigned long long key =
+                ((unsigned long long)orderable(capped) << 32) | (0xffffffffu - (uint32_t)r);
+            best = key > best ? key : best;
+        }
+    }
+    if (lane == 0) wkey[wave] = best;
+    __syncthreads();
+    if (tid == 0) {
+        unsigned long long b = 0ull;
+        for (int w = 0; w < kHeadThreads / 64; ++w) b = wkey[w] > b ? wkey[w] : b;
+        atomicMax(&st->key, b);
+        __threadfence();
+        last = atomicAdd(&st->done, 1u) == gridDim.x - 1 ? 1u : 0u;
+    }
+    __syncthreads();
+    if (tid == 0 && last) {
+        __threadfence();
+        const unsigned long long key = atomicAdd(&st->key, 0ull);
+        const int token = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
+        const int step = st->step;
+        if (tokens_out && step >= 0 && step < tokens_cap) tokens_out[step] = token;
+        st->token = (step >= 0 && step < n_force) ? force[step] : token;
+        st->pos += 1;
+        st->step += 1;
+        st->key = 0ull;
+        st->done = 0u;
+    }
+}
+
+}  // namespace
+
+int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
+                       const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream) {
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, stream, x, y, emb, st, w,
+                       h, h_dtype, n, eps);
+    return check_launch("nb_add_rmsnorm");
+}
+
+int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                          const float* sin_t, const nb_decode_state* st, float* work,
+                          unsigned* done, void* out, int out_dtype, int n_head, int head_dim,
+                          int ctx, hipStream_t stream) {
+    hipLaunchKernelGGL(attention_step_kernel, dim3(n_head, kAttnSplits), dim3(kAttnThreads), 0,
+                       stream, qkv, k_cache, v_cache, cos_t, sin_t, st, work, done, out, out_dtype,
+                       n_head, head_dim, ctx);
+    return check_launch("nb_attention_step");
+}
+
+int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t stream) {
+    const int blocks = std::min(1024, (n + 255) / 256);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(blocks), dim3(256), 0, stream, gu, act, dtype, n);
+    return check_launch("nb_silu_mul");
+}
+
+int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* st,
+                          int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
+                          int V, int C, hipStream_t stream) {
+    const int blocks = std::min(1024, (V + 3) / 4);
+    hipLaunchKernelGGL(lm_head_argmax_kernel, dim3(blocks), dim3(kHeadThreads), 0, stream,
+                       static_cast<const bf16_bits*>(h), static_cast<const bf16_bits*>(emb), logits,
+                       st, tokens_out, tokens_cap, force, n_force, V, C);
+    return check_launch("nb_lm_head_argmax");
+}
+
+int attention_work_floats(int n_head) { return n_head * kAttnSplits * (kMaxHeadDim + 2); }
+int attention_max_head_dim() { return kMaxHeadDim; }
+int lm_head_max_c() { return kHeadMaxC; }
+
+}  // namespace nb

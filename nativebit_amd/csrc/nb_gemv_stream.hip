@@ -347,13 +347,15 @@ void gemv_stream_kernel(
         int lchunk = c_first;
         bool lvalid = true;
 
-        // Loads the chunk at the load cursor into ring slot `slot` (always:
-        // after the last chunk the cursor stays put and the load repeats),
-        // records where it belongs and moves the cursor to chunk `next`
-        // (taken from the counter beforehand).  In a problem's partial last
+        // Loads the chunk at the load cursor into ring slot `slot`, records
+        // where it belongs and moves the cursor to chunk `next` (taken from
+        // the counter beforehand); past the wave's last chunk it marks the
+        // slot invalid and loads nothing.  In a problem's partial last
         // chunk, lanes past the end of the stream re-read its last 16 bytes
         // (their blocks are not live).
         auto issue = [&](int slot, Meta& m, int next) {
+            m.valid = lvalid;
+            if (!lvalid) return;  // past the wave's last chunk: no load
             const int lc = lchunk - LP.chunk_begin;
             const uint32_t dst = __builtin_amdgcn_readfirstlane(my_ring_lds + slot * kSlotBytes);
             const uint8_t* ip = LP.packed + (int64_t)lc * kChunkIdxBytes + 16 * lane;
@@ -377,10 +379,8 @@ void gemv_stream_kernel(
             }
             m.li = li;
             m.lc = lc;
-            m.valid = lvalid;
-            if (!lvalid) return;
             if (next >= C1) {
-                lvalid = false;  // repeat this chunk's addresses from now on
+                lvalid = false;  // the wave's last chunk
             } else {
                 lchunk = next;
                 while (lchunk >= LP.chunk_end) read_prob(pl, ++li, LP);
@@ -494,14 +494,22 @@ void gemv_stream_kernel(
         // chunk kDepth ahead, and compute -- kDepth chunks are in flight
         // during the arithmetic.  Validity is monotonic: the first invalid
         // slot ends the wave's work.  The loop issues no other vector-memory
-        // instruction, so the vmcnt waits count ring loads exactly.
-        constexpr int kAhead = (kDepth - 1) * kLoadsPerChunk;
+        // instruction, so the vmcnt waits count ring loads exactly (each
+        // valid slot holds kLoadsPerChunk loads).
         Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
-        auto step = [&](int slot, Meta& m) {
+        // `after` = valid slots loaded after this one (their loads may stay
+        // in flight).
+        auto step = [&](int slot, Meta& m, int after) {
             const int next = lvalid ? grab() : C1;
             u32x4_t xv[16];
             const Lane L = prepare(m, xv);
-            wait_vm<kAhead>();
+            if (after == 2) {
+                wait_vm<2 * kLoadsPerChunk>();
+            } else if (after == 1) {
+                wait_vm<kLoadsPerChunk>();
+            } else {
+                wait_vm<0>();
+            }
             const SlotRegs r = read_slot(slot);
             wait_lds();
             const Meta cur = m;
@@ -513,25 +521,23 @@ void gemv_stream_kernel(
             issue(1, mb, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
-                step(0, ma);
+                step(0, ma, mb.valid ? 1 : 0);
                 if (!mb.valid) break;
-                step(1, mb);
+                step(1, mb, ma.valid ? 1 : 0);
             }
         } else {
             issue(1, mb, lvalid ? grab() : C1);
             issue(2, mc, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
-                step(0, ma);
+                step(0, ma, (int)mb.valid + (int)mc.valid);
                 if (!mb.valid) break;
-                step(1, mb);
+                step(1, mb, (int)mc.valid + (int)ma.valid);
                 if (!mc.valid) break;
-                step(2, mc);
+                step(2, mc, (int)ma.valid + (int)mb.valid);
             }
         }
-        // the loads issued past the wave's last chunk land before the
-        // workgroup (and its LDS) can end
-        wait_vm<0>();
+        wait_vm<0>();  // (nothing is in flight here; kept as a guard)
     }
 
     // ---- write the range's outputs (coalesced, after every wave is done) --

@@ -87,4 +87,20 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
                    int w_dtype, int64_t total, int64_t num_blocks, int bits,
                    int n_entries, int block_size, hipStream_t stream);
 
+
+// Decode-step kernels (nb_decode.hip).
+int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
+                       const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream);
+int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                          const float* sin_t, const nb_decode_state* st, float* work,
+                          unsigned* done, void* out, int out_dtype, int n_head, int head_dim,
+                          int ctx, hipStream_t stream);
+int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t stream);
+int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* st,
+                          int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
+                          int V, int C, hipStream_t stream);
+int attention_work_floats(int n_head);
+int attention_max_head_dim();
+int lm_head_max_c();
+
 }  // namespace nb

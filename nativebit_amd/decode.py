@@ -1,0 +1,220 @@
+"""Greedy decode of a packed NativeBit model as one HIP graph per token.
+
+The same model as ``nativebit_amd.model.PackedGPT`` (inference/
+generate_torch.py:135-162), run as a fixed sequence of gfx950 launches per
+token: per layer nb_add_rmsnorm -> q|k|v GEMV -> nb_attention_step -> o
+GEMV -> nb_add_rmsnorm -> gate|up GEMV -> nb_silu_mul -> down GEMV, then the
+final norm and nb_lm_head_argmax.  The position and the current token live
+in device memory, so the step is captured once in a HIP graph and replayed
+per token with no host round trip (the reference synchronises on
+``int(logits.argmax())`` every token, generate_torch.py:311).
+
+Numerics: the residual stream, norms, attention and KV cache are fp32 as in
+the reference; the activations handed to the packed GEMVs are rounded to
+bf16 (the bf16 path of inference/eval_ppl.py:149-174, with bf16-rounded
+codebook entries and fp32 accumulation); the tied head reads a bf16 copy of
+the embedding.  The prompt is fed through the same step with teacher
+forcing.
+"""
+from __future__ import annotations
+
+import ctypes
+import time
+
+import torch
+
+from . import _lib, ops
+from .model import PackedGPT, precompute_rope
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _fuse_rows(layers):
+    """One packed layer holding the rows of several (same in_features, rows
+    never share a block): streams and codebooks concatenated."""
+    packed = torch.cat([l.packed_indices for l in layers]).contiguous()
+    cb = torch.cat([l.codebook for l in layers]).contiguous()
+    return packed, cb, sum(l.out_features for l in layers), layers[0].in_features
+
+
+class DecodeEngine:
+    """Device-resident greedy decoder for one sequence (batch 1)."""
+
+    def __init__(self, model: PackedGPT, max_steps: int | None = None):
+        cfg = model.cfg
+        dev = model.embedding.weight.device
+        if dev.type != "cuda":
+            raise ValueError("DecodeEngine runs on a ROCm GPU")
+        self.model, self.cfg, self.dev = model, cfg, dev
+        C, F, H = cfg.n_embd, cfg.ffn_hidden, cfg.n_head
+        D = C // H
+        self.C, self.F, self.H, self.D = C, F, H, D
+        self.V = model.embedding.weight.shape[0]
+        self.ctx = cfg.context_len
+        self.max_steps = max_steps or cfg.context_len
+        f32, bf16 = torch.float32, torch.bfloat16
+        z = lambda *s, dt=f32: torch.zeros(*s, dtype=dt, device=dev)  # noqa: E731
+        self.x = z(C)
+        self.h = z(C, dt=bf16)
+        self.qkv = z(3 * C)
+        self.att = z(C, dt=bf16)
+        self.o = z(C)
+        self.gu = z(2 * F)
+        self.act = z(F, dt=bf16)
+        self.d = z(C)
+        self.logits = z(self.V)
+        self.emb_f32 = model.embedding.weight.detach().to(f32).contiguous()
+        self.emb_bf16 = self.emb_f32.to(bf16).contiguous()
+        cos, sin = precompute_rope(D, self.ctx, cfg.rope_theta)
+        self.cos, self.sin = cos.to(dev).contiguous(), sin.to(dev).contiguous()
+        self.kc = z(cfg.n_layers, H, self.ctx, D)
+        self.vc = z(cfg.n_layers, H, self.ctx, D)
+        lib = _lib.load()
+        self.work = z(int(lib.nb_attention_work_floats(H)))
+        self.done = z(H, dt=torch.int32)
+        self.state_t = z(32, dt=torch.uint8)
+        self.tokens = z(self.max_steps, dt=torch.int32)
+        self.force = z(self.max_steps, dt=torch.int32)
+        self.n_force = 0
+        self.norms = []
+        self.gemvs = []
+        self._keep = []
+        for blk in model.blocks:
+            qkv_p, qkv_c, qkv_n, _ = _fuse_rows([blk.attn.qkv])
+            gu_p, gu_c, gu_n, _ = _fuse_rows([blk.ffn.gate, blk.ffn.up])
+            self._keep += [gu_p, gu_c]
+            o, dn = blk.attn.out_proj, blk.ffn.down
+            self.gemvs.append((
+                ops.GemvBatch([(self.h, qkv_p, qkv_c, self.qkv, qkv_n, C)]),
+                ops.GemvBatch([(self.att, o.packed_indices, o.codebook, self.o, C, C)]),
+                ops.GemvBatch([(self.h, gu_p, gu_c, self.gu, 2 * F, C)]),
+                ops.GemvBatch([(self.act, dn.packed_indices, dn.codebook, self.d, C, F)]),
+            ))
+            self.norms.append((blk.ln1.weight.detach().float().contiguous(),
+                               blk.ln2.weight.detach().float().contiguous()))
+        self.ln_f = model.ln_f.weight.detach().float().contiguous()
+        self.eps = float(cfg.norm_eps)
+        self.graph = None
+        self.fed = 0
+
+    # -- state ------------------------------------------------------------
+    def reset(self, prompt_tokens):
+        """Start a sequence: position 0, first prompt token fed, the rest
+        forced."""
+        prompt = [int(t) for t in prompt_tokens]
+        if not prompt:
+            raise ValueError("empty prompt")
+        if min(prompt) < 0 or max(prompt) >= self.V:
+            raise ValueError(f"prompt token outside 0..{self.V - 1}")
+        if len(prompt) > self.max_steps:
+            raise ValueError("prompt longer than max_steps")
+        st = _lib.DecodeState(0, 0, prompt[0], 0, 0)
+        host = torch.frombuffer(bytearray(bytes(st)), dtype=torch.uint8)
+        self.state_t[: ctypes.sizeof(st)].copy_(host)
+        self.n_force = len(prompt) - 1
+        if self.n_force:
+            self.force[: self.n_force].copy_(torch.tensor(prompt[1:], dtype=torch.int32))
+        self.kc.zero_()
+        self.vc.zero_()
+        self.done.zero_()
+        self.fed = 0
+        self.graph = None  # n_force is baked into the launch
+
+    # -- one step ---------------------------------------------------------
+    def _launch(self):
+        lib = _lib.load()
+        s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        ck = _lib.check
+        st = _ptr(self.state_t)
+        C, F = self.C, self.F
+        BF = _lib.NB_BF16
+        for l, (g_qkv, g_o, g_gu, g_d) in enumerate(self.gemvs):
+            ln1, ln2 = self.norms[l]
+            if l == 0:
+                ck(lib.nb_add_rmsnorm(_ptr(self.x), None, _ptr(self.emb_f32), st, _ptr(ln1),
+                                      _ptr(self.h), BF, C, self.eps, s))
+            else:
+                ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.d), None, st, _ptr(ln1),
+                                      _ptr(self.h), BF, C, self.eps, s))
+            g_qkv.run()
+            ck(lib.nb_attention_step(_ptr(self.qkv), _ptr(self.kc[l]), _ptr(self.vc[l]),
+                                     _ptr(self.cos), _ptr(self.sin), st, _ptr(self.work),
+                                     _ptr(self.done), _ptr(self.att), BF, self.H, self.D,
+                                     self.ctx, s))
+            g_o.run()
+            ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.o), None, st, _ptr(ln2), _ptr(self.h),
+                                  BF, C, self.eps, s))
+            g_gu.run()
+            ck(lib.nb_silu_mul(_ptr(self.gu), _ptr(self.act), BF, F, s))
+            g_d.run()
+        ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.d), None, st, _ptr(self.ln_f), _ptr(self.h),
+                              BF, C, self.eps, s))
+        ck(lib.nb_lm_head_argmax(_ptr(self.h), _ptr(self.emb_bf16), _ptr(self.logits), st,
+                                 _ptr(self.tokens), self.max_steps, _ptr(self.force), self.n_force,
+                                 self.V, C, s))
+
+    def _advance(self, n):
+        if self.fed + n > min(self.ctx, self.max_steps):
+            raise ValueError(f"{self.fed} + {n} steps exceed the context ({self.ctx}) or "
+                             f"max_steps ({self.max_steps})")
+        self.fed += n
+
+    def step(self):
+        """Feed the current token (eagerly, no graph)."""
+        self._advance(1)
+        self._launch()
+
+    def capture(self):
+        """Capture one step in a HIP graph (replayed by run())."""
+        g = torch.cuda.CUDAGraph()
+        # the graph records the launches only; warm the libraries first
+        with torch.cuda.graph(g):
+            self._launch()
+        self.graph = g
+
+    def run(self, n_steps: int):
+        self._advance(n_steps)
+        if self.graph is None:
+            self.capture()
+        for _ in range(n_steps):
+            self.graph.replay()
+
+    def state(self) -> dict:
+        st = _lib.DecodeState.from_buffer_copy(bytes(self.state_t[:24].cpu().numpy()))
+        return {"pos": st.pos, "token": st.token, "step": st.step, "key": st.key, "done": st.done}
+
+    # -- whole sequences ----------------------------------------------------
+    @torch.no_grad()
+    def generate(self, prompt_tokens, n_generate: int) -> list:
+        """Greedy continuation: the n_generate tokens the reference's loop
+        produces (generate_torch.py:298-313)."""
+        n_prompt = len(prompt_tokens)
+        if n_prompt + n_generate > min(self.ctx, self.max_steps):
+            raise ValueError("prompt + generated tokens exceed the context")
+        self.reset(prompt_tokens)
+        self.run(n_prompt + n_generate - 1)
+        torch.cuda.synchronize()
+        return self.tokens[n_prompt - 1: n_prompt - 1 + n_generate].cpu().tolist()
+
+    @torch.no_grad()
+    def benchmark(self, prompt_tokens, n_generate: int, n_runs: int = 3) -> dict:
+        """Decode tokens/s after the prompt (timed like generate_torch.py:
+        280-320, but with the step graph replayed back to back)."""
+        n_prompt = len(prompt_tokens)
+        self.reset(prompt_tokens)
+        self.capture()
+        times = []
+        for _ in range(n_runs):
+            self.reset(prompt_tokens)
+            self.capture()
+            self.run(n_prompt)          # prompt (teacher forced) + first token chosen
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            self.run(n_generate - 1)    # the rest of the continuation
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {"generate_tps": (n_generate - 1) / t, "per_token_ms": t / (n_generate - 1) * 1e3,
+                "runs": len(times)}

@@ -1,0 +1,158 @@
+"""CPU restatement of the reference's packed decoder -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/`` (and ``bench.py``'s ``cpu_baseline`` leg) may import this
+module, as the checker.  It restates inference/generate_torch.py:29-162 and
+269-320 in fp32 torch on the CPU, with every packed linear expanded to its
+dense weight through the oracle's exact gather (``oracle.dequant``):
+
+* ``Dense`` linears from (packed stream, codebook) -- W[r, c] =
+  cb[(r*K + c) // BS][index], the gather of triton_kernel.py:268-273;
+* ``forward(idx, caches, pos)`` with the KV-cache path (generate_torch.py:
+  80-98) or, without caches, causal attention over the whole sequence;
+* ``greedy(prompt, n)``: the benchmark loop's greedy continuation
+  (generate_torch.py:298-313).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import oracle as O
+
+
+def dense_weight(packed, codebook, out_f, in_f, block_size=128, bits=3) -> torch.Tensor:
+    """fp32 (out_f, in_f) weight by the exact gather."""
+    p = np.asarray(packed, dtype=np.uint8)
+    cb = np.asarray(codebook, dtype=np.float32)
+    total = out_f * in_f
+    idx = O.unpack(p, cb.shape[0] * block_size, bits)
+    return torch.from_numpy(O.dequant(idx, cb, block_size, total).reshape(out_f, in_f))
+
+
+def rmsnorm(x, w, eps):
+    norm = torch.sqrt(x.float().pow(2).mean(-1, keepdim=True) + eps)
+    return x.float() / norm * w.float()
+
+
+def rope_tables(dim, max_len, theta=10000.0):
+    freqs = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
+    t = torch.arange(max_len, dtype=torch.float32)
+    f = torch.outer(t, freqs)
+    return torch.cos(f), torch.sin(f)
+
+
+def rope(x, cos, sin, pos0):
+    T = x.shape[2]
+    c = cos[pos0:pos0 + T][None, None].repeat_interleave(2, dim=-1)
+    s = sin[pos0:pos0 + T][None, None].repeat_interleave(2, dim=-1)
+    x1, x2 = x[..., ::2], x[..., 1::2]
+    rot = torch.stack((-x2, x1), dim=-1).reshape(x.shape)
+    return x * c + rot * s
+
+
+class DecoderRef:
+    """The packed decoder with dense fp32 weights on the CPU."""
+
+    def __init__(self, cfg, layers, embedding, norms, ln_f):
+        """layers: per block dict name -> (out, in) fp32 weight for qkv,
+        out_proj, gate, up, down; norms: per block (ln1 w, ln2 w)."""
+        self.cfg = cfg
+        self.layers = layers
+        self.emb = embedding.float()
+        self.norms = norms
+        self.ln_f = ln_f.float()
+        self.D = cfg.n_embd // cfg.n_head
+        self.cos, self.sin = rope_tables(self.D, cfg.context_len, cfg.rope_theta)
+
+    @classmethod
+    def from_model(cls, model):
+        """Dense copy of a nativebit_amd.model.PackedGPT (weights read back
+        from its packed buffers)."""
+        layers, norms = [], []
+        for blk in model.blocks:
+            lin = {}
+            for name, pl in (("qkv", blk.attn.qkv), ("out_proj", blk.attn.out_proj),
+                             ("gate", blk.ffn.gate), ("up", blk.ffn.up), ("down", blk.ffn.down)):
+                lin[name] = dense_weight(pl.packed_indices.cpu().numpy(), pl.codebook.cpu().numpy(),
+                                         pl.out_features, pl.in_features, pl.block_size, pl.bits)
+            layers.append(lin)
+            norms.append((blk.ln1.weight.detach().cpu().float(), blk.ln2.weight.detach().cpu().float()))
+        return cls(model.cfg, layers, model.embedding.weight.detach().cpu().float(), norms,
+                   model.ln_f.weight.detach().cpu().float())
+
+    def init_cache(self):
+        c = self.cfg
+        return [(torch.zeros(1, c.n_head, c.context_len, self.D),
+                 torch.zeros(1, c.n_head, c.context_len, self.D)) for _ in range(c.n_layers)], 0
+
+    @torch.no_grad()
+    def forward(self, idx, cache=None, pos0=0, weight_dtype=None, act_dtype=None,
+                head_dtype=None):
+        """Logits (B, T, V).  With ``cache`` = (per-layer (k, v), length) the
+        cache path is used and updated in place; weight_dtype/act_dtype
+        (e.g. torch.bfloat16) round linear weights / inputs, head_dtype the
+        final hidden state and the tied embedding of the head, to emulate a
+        reduced-precision path (products and sums stay fp32)."""
+        c = self.cfg
+        H, D = c.n_head, self.D
+        x = self.emb[idx]
+        B, T, C = x.shape
+
+        def lin(v, w):
+            if weight_dtype is not None:
+                w = w.to(weight_dtype).float()
+            if act_dtype is not None:
+                v = v.to(act_dtype).float()
+            return v @ w.T
+
+        for l, L in enumerate(self.layers):
+            h = rmsnorm(x, self.norms[l][0], c.norm_eps)
+            q, k, v = lin(h, L["qkv"]).chunk(3, dim=-1)
+            q = q.reshape(B, T, H, D).transpose(1, 2)
+            k = k.reshape(B, T, H, D).transpose(1, 2)
+            v = v.reshape(B, T, H, D).transpose(1, 2)
+            p0 = pos0 if cache is None else cache[1]
+            q, k = rope(q, self.cos, self.sin, p0), rope(k, self.cos, self.sin, p0)
+            if cache is not None:
+                kb, vb = cache[0][l]
+                kb[:, :, p0:p0 + T] = k
+                vb[:, :, p0:p0 + T] = v
+                n = p0 + T
+                att = (q * D ** -0.5) @ kb.transpose(-1, -2)
+                qp = p0 + torch.arange(T)
+                kp = torch.arange(kb.shape[2])
+                mask = (kp[None, :] <= qp[:, None]) & (kp[None, :] < n)
+                att = att.masked_fill(~mask[None, None], torch.finfo(att.dtype).min)
+                o = F.softmax(att, dim=-1) @ vb
+            else:
+                att = (q * D ** -0.5) @ k.transpose(-1, -2)
+                mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
+                att = att.masked_fill(~mask[None, None], float("-inf"))
+                o = F.softmax(att, dim=-1) @ v
+            x = x + lin(o.transpose(1, 2).reshape(B, T, C), L["out_proj"])
+            h2 = rmsnorm(x, self.norms[l][1], c.norm_eps)
+            x = x + lin(F.silu(lin(h2, L["gate"])) * lin(h2, L["up"]), L["down"])
+        if cache is not None:
+            cache = (cache[0], cache[1] + T)
+        x = rmsnorm(x, self.ln_f, c.norm_eps)
+        e = self.emb
+        if head_dtype is not None:
+            x, e = x.to(head_dtype).float(), e.to(head_dtype).float()
+        logits = 30.0 * torch.tanh((x @ e.T) / 30.0)
+        return logits, cache
+
+    @torch.no_grad()
+    def greedy(self, prompt, n_generate):
+        """Greedy continuation (generate_torch.py:298-313)."""
+        cache = self.init_cache()
+        logits, cache = self.forward(torch.tensor([list(prompt)]), cache)
+        tok = int(logits[0, -1].argmax())
+        out = []
+        for _ in range(n_generate):
+            out.append(tok)
+            logits, cache = self.forward(torch.tensor([[tok]]), cache)
+            tok = int(logits[0, -1].argmax())
+        return out
