@@ -197,8 +197,9 @@ int nb_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_s
  * One token of causal self-attention for all heads at position state->pos:
  * RoPE of the query and key (pairs (2i, 2i+1), angle pos * theta^(-2i/D),
  * tables cos/sin of [ctx][D/2] fp32), append of the rotated key and the
- * value to the caches ([n_head][ctx][D] fp32 each), softmax(q k^T / sqrt(D))
- * over positions 0..pos, output [n_head * D] (NB_F32 or NB_BF16).  A
+ * value to the caches (fp32; keys transposed, [n_head][D][ctx], values
+ * [n_head][ctx][D]), softmax(q k^T / sqrt(D)) over positions 0..pos,
+ * output [n_head * D] (NB_F32 or NB_BF16).  ctx <= 1024, D <= 256.  A
  * position outside 0..ctx-1 leaves caches and output untouched.
  * qkv: [3 * n_head * D] fp32, q | k | v.  work: nb_attention_work_floats()
  * floats; done: n_head uint32 counters, zero before the first call (each

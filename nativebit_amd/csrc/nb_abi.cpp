@@ -350,6 +350,9 @@ int nb_attention_step(const float* qkv, float* k_cache, float* v_cache, const fl
                       int ctx, void* stream) {
     const char* fn = "nb_attention_step";
     if (n_head < 1 || ctx < 1) return fail(NB_EINVAL, "%s: n_head=%d ctx=%d", fn, n_head, ctx);
+    if (ctx > attention_max_ctx()) {
+        return fail(NB_EUNSUPPORTED, "%s: ctx=%d > %d", fn, ctx, attention_max_ctx());
+    }
     if (head_dim < 2 || head_dim % 2 || head_dim > attention_max_head_dim()) {
         return fail(NB_EUNSUPPORTED, "%s: head_dim=%d (even, <= %d)", fn, head_dim,
                     attention_max_head_dim());

@@ -38,6 +38,21 @@ __device__ __forceinline__ void store_act(void* p, int dtype, int64_t i, float v
     }
 }
 
+// Cross-workgroup hand-over inside one launch.  Values another workgroup
+// will read are written and read with agent-scope atomic accesses, which
+// are coherent across the XCDs' separate L2 caches, and the writer waits
+// for its stores to complete (vmcnt counts stores on gfx9) before it bumps
+// the counter that publishes them.  A __threadfence() would instead write
+// back the whole L2 of the XCD, which costs tens of microseconds when the
+// decode step leaves much dirty data behind.
+__device__ __forceinline__ void put_agent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float get_agent(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -99,17 +114,24 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(
 // ---------------------------------------------------------------------------
 // attention for one new token, split over positions
 // ---------------------------------------------------------------------------
-// Grid (n_head, kAttnSplits); block 256 threads = 4 waves.  Workgroup
-// (hd, s) takes positions s, s + S, s + 2S, ... <= pos; each wave takes one
-// position at a time, its 64 lanes covering head_dim in pairs.  Partial
-// softmax state (max, sum, weighted V) goes to the workspace; the last
+// Caches: keys transposed, [n_head][D][ctx] (position fastest), values
+// [n_head][ctx][D].  Grid (n_head, kAttnSplits); workgroup (hd, s) takes the
+// contiguous positions [s*Lp, min(pos+1, (s+1)*Lp)), Lp = ceil((pos+1)/S)
+// <= 64.  Scores: lane i takes position t0 + i and each of the 4 waves a
+// quarter of the head dimension, so every key load is 64 consecutive
+// positions (coalesced); the quarters are summed in wave order.  Softmax
+// partials (max, sum) and the weighted sum of values (thread d takes
+// dimension d, reading value rows whole) go to the workspace; the last
 // workgroup of a head (atomic counter) combines the splits in split order.
-// Every workgroup rotates the new query and key itself and uses the new
-// key/value directly at t == pos, so only workgroup (hd, 0) writes the cache
-// and nothing reads what another workgroup writes in the same launch.
+// Every workgroup rotates the new query and key itself; the workgroup whose
+// range holds pos uses the new key/value directly and is the only one that
+// writes them to the caches, so nothing reads what another workgroup writes
+// in the same launch.
 constexpr int kAttnSplits = 16;
 constexpr int kAttnThreads = 256;
+constexpr int kAttnMaxSplitLen = 64;
 constexpr int kMaxHeadDim = 256;
+constexpr int kMaxCtx = kAttnSplits * kAttnMaxSplitLen;
 
 __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     const float* __restrict__ qkv, float* __restrict__ k_cache, float* __restrict__ v_cache,
@@ -117,8 +139,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     const nb_decode_state* __restrict__ st, float* __restrict__ work, unsigned* __restrict__ done,
     void* __restrict__ out, int out_dtype, int n_head, int D, int ctx) {
     __shared__ float q[kMaxHeadDim], kn[kMaxHeadDim], vn[kMaxHeadDim];
-    __shared__ float wm[kAttnThreads / 64], wl[kAttnThreads / 64];
-    __shared__ float wo[kAttnThreads / 64][kMaxHeadDim];
+    __shared__ float sc[kAttnThreads / 64][kAttnMaxSplitLen];
+    __shared__ float p[kAttnMaxSplitLen];
+    __shared__ float ml[2];
     __shared__ unsigned last;
     const int hd = blockIdx.x, s = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -126,6 +149,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     if (pos < 0 || pos >= ctx) return;  // past the cache: nothing to do
     const int C = n_head * D;
     const float scale = 1.0f / sqrtf((float)D);
+    const int n = pos + 1;
+    const int Lp = (n + kAttnSplits - 1) / kAttnSplits;
+    const int t0 = min(n, s * Lp), t1 = min(n, t0 + Lp);
     // RoPE of the new query and key (pairs (2i, 2i+1) rotated by angle i)
     for (int i = tid; i < D / 2; i += kAttnThreads) {
         const float c = cos_t[(int64_t)pos * (D / 2) + i], sn = sin_t[(int64_t)pos * (D / 2) + i];
@@ -139,78 +165,84 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     }
     for (int d = tid; d < D; d += kAttnThreads) vn[d] = qkv[2 * C + hd * D + d];
     __syncthreads();
-    if (s == 0) {
+    const float* kt = k_cache + (int64_t)hd * D * ctx;  // [D][ctx]
+    const float* vc = v_cache + (int64_t)hd * ctx * D;  // [ctx][D]
+    if (pos >= t0 && pos < t1) {
         for (int d = tid; d < D; d += kAttnThreads) {
-            k_cache[((int64_t)hd * ctx + pos) * D + d] = kn[d];
+            k_cache[((int64_t)hd * D + d) * ctx + pos] = kn[d];
             v_cache[((int64_t)hd * ctx + pos) * D + d] = vn[d];
         }
     }
-    // this wave's positions: t = s + S * (wave + 4 j)
-    float m = -INFINITY, l = 0.f;
-    float o0 = 0.f, o1 = 0.f, o2 = 0.f, o3 = 0.f;  // dims lane, lane+64, +128, +192
-    const float* kc = k_cache + (int64_t)hd * ctx * D;
-    const float* vc = v_cache + (int64_t)hd * ctx * D;
-    for (int t = s + kAttnSplits * wave; t <= pos; t += kAttnSplits * (kAttnThreads / 64)) {
-        const float* kr = t == pos ? kn : kc + (int64_t)t * D;
-        const float* vr = t == pos ? vn : vc + (int64_t)t * D;
-        float part = 0.f;
-        for (int d = lane; d < D; d += 64) part += q[d] * kr[d];
-        const float sc = wave_sum(part);
-        const float mn = fmaxf(m, sc);
-        const float a = __expf(m - mn), b = __expf(sc - mn);
-        l = l * a + b;
-        if (lane < D) o0 = o0 * a + b * vr[lane];
-        if (lane + 64 < D) o1 = o1 * a + b * vr[lane + 64];
-        if (lane + 128 < D) o2 = o2 * a + b * vr[lane + 128];
-        if (lane + 192 < D) o3 = o3 * a + b * vr[lane + 192];
-        m = mn;
+    // partial scores of this wave's quarter of the dimensions
+    const int t = t0 + lane;
+    const int dq = (D + 3) / 4;
+    const int d0 = wave * dq, d1 = min(D, d0 + dq);
+    float part = 0.f;
+    if (t < t1) {
+        if (t == pos) {
+            for (int d = d0; d < d1; ++d) part += q[d] * kn[d];
+        } else {
+#pragma unroll 8
+            for (int d = d0; d < d1; ++d) part += q[d] * kt[(int64_t)d * ctx + t];
+        }
     }
-    // combine the 4 waves of this workgroup
-    if (lane == 0) {
-        wm[wave] = m;
-        wl[wave] = l;
-    }
-    wo[wave][lane] = o0;
-    wo[wave][lane + 64] = o1;
-    wo[wave][lane + 128] = o2;
-    wo[wave][lane + 192] = o3;
+    sc[wave][lane] = part;
     __syncthreads();
     float* wk = work + ((int64_t)hd * kAttnSplits + s) * (kMaxHeadDim + 2);
-    if (tid < D) {
-        float M = -INFINITY;
-        for (int w = 0; w < kAttnThreads / 64; ++w) M = fmaxf(M, wm[w]);
-        float L = 0.f, O = 0.f;
-        for (int w = 0; w < kAttnThreads / 64; ++w) {
-            const float f = wm[w] == -INFINITY ? 0.f : __expf(wm[w] - M);
-            L += f * wl[w];
-            O += f * wo[w][tid];
+    if (wave == 0) {
+        float score = -INFINITY;
+        if (t < t1) {
+            score = 0.f;
+            for (int w = 0; w < kAttnThreads / 64; ++w) score += sc[w][lane];
         }
-        wk[2 + tid] = O;
-        if (tid == 0) {
-            wk[0] = M;
-            wk[1] = L;
+        const float m = wave_max(score);
+        const float e = t < t1 ? __expf(score - m) : 0.f;
+        const float l = wave_sum(e);
+        p[lane] = e;
+        if (lane == 0) {
+            ml[0] = m;
+            ml[1] = l;
         }
     }
-    // the last workgroup of this head combines the splits
-    __threadfence();
     __syncthreads();
-    if (tid == 0) last = atomicAdd(done + hd, 1u) == kAttnSplits - 1 ? 1u : 0u;
+    for (int d = tid; d < D; d += kAttnThreads) {
+        float o = 0.f;
+        for (int i = 0; i < t1 - t0; ++i) {
+            const int tt = t0 + i;
+            o += p[i] * (tt == pos ? vn[d] : vc[(int64_t)tt * D + d]);
+        }
+        put_agent(wk + 2 + d, o);
+    }
+    if (tid == 0) {
+        put_agent(wk, ml[0]);
+        put_agent(wk + 1, ml[1]);
+    }
+    // the last workgroup of this head combines the splits
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) {
+        last = __hip_atomic_fetch_add(done + hd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       kAttnSplits - 1
+                   ? 1u
+                   : 0u;
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
-    if (tid < D) {
-        const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
+    const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
+    for (int d = tid; d < D; d += kAttnThreads) {
         float M = -INFINITY;
-        for (int j = 0; j < kAttnSplits; ++j) M = fmaxf(M, __builtin_nontemporal_load(base + j * (kMaxHeadDim + 2)));
+        for (int j = 0; j < kAttnSplits; ++j) {
+            M = fmaxf(M, get_agent(base + j * (kMaxHeadDim + 2)));
+        }
         float L = 0.f, O = 0.f;
         for (int j = 0; j < kAttnSplits; ++j) {
-            const float* p = base + j * (kMaxHeadDim + 2);
-            const float mj = __builtin_nontemporal_load(p);
+            const float* pj = base + j * (kMaxHeadDim + 2);
+            const float mj = get_agent(pj);
             const float f = mj == -INFINITY ? 0.f : __expf(mj - M);
-            L += f * __builtin_nontemporal_load(p + 1);
-            O += f * __builtin_nontemporal_load(p + 2 + tid);
+            L += f * get_agent(pj + 1);
+            O += f * get_agent(pj + 2 + d);
         }
-        store_act(out, out_dtype, hd * D + tid, O / L);
+        store_act(out, out_dtype, hd * D + d, O / L);
     }
     if (tid == 0) done[hd] = 0u;  // ready for the next step
 }
@@ -284,12 +316,11 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
         unsigned long long b = 0ull;
         for (int w = 0; w < kHeadThreads / 64; ++w) b = wkey[w] > b ? wkey[w] : b;
         atomicMax(&st->key, b);
-        __threadfence();
+        wait_stores();  // the max is performed before the count publishes it
         last = atomicAdd(&st->done, 1u) == gridDim.x - 1 ? 1u : 0u;
     }
     __syncthreads();
     if (tid == 0 && last) {
-        __threadfence();
         const unsigned long long key = atomicAdd(&st->key, 0ull);
         const int token = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
         const int step = st->step;
@@ -339,6 +370,7 @@ int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_deco
 
 int attention_work_floats(int n_head) { return n_head * kAttnSplits * (kMaxHeadDim + 2); }
 int attention_max_head_dim() { return kMaxHeadDim; }
+int attention_max_ctx() { return kMaxCtx; }
 int lm_head_max_c() { return kHeadMaxC; }
 
 }  // namespace nb

@@ -101,6 +101,7 @@ int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_deco
                           int V, int C, hipStream_t stream);
 int attention_work_floats(int n_head);
 int attention_max_head_dim();
+int attention_max_ctx();
 int lm_head_max_c();
 
 }  // namespace nb

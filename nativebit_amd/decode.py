@@ -69,7 +69,7 @@ class DecodeEngine:
         self.emb_bf16 = self.emb_f32.to(bf16).contiguous()
         cos, sin = precompute_rope(D, self.ctx, cfg.rope_theta)
         self.cos, self.sin = cos.to(dev).contiguous(), sin.to(dev).contiguous()
-        self.kc = z(cfg.n_layers, H, self.ctx, D)
+        self.kc = z(cfg.n_layers, H, D, self.ctx)   # keys transposed: [layer][head][dim][pos]
         self.vc = z(cfg.n_layers, H, self.ctx, D)
         lib = _lib.load()
         self.work = z(int(lib.nb_attention_work_floats(H)))

@@ -114,19 +114,18 @@ def torch_attention(qkv, kc, vc, pos, H, D, ctx):
     return out, kc, vc
 
 
-@pytest.mark.parametrize("H,D", [(20, 128), (4, 64), (2, 32)])
-def test_attention_step(dev, H, D):
+@pytest.mark.parametrize("H,D,ctx", [(20, 128, 80), (4, 64, 80), (2, 32, 80), (20, 128, 1024)])
+def test_attention_step(dev, H, D, ctx):
     lib = _lib.load()
-    ctx = 80
     g = torch.Generator().manual_seed(H * 100 + D)
     kc = torch.randn(H, ctx, D, generator=g)
     vc = torch.randn(H, ctx, D, generator=g)
     cos, sin = precompute_rope(D, ctx)
     work = torch.zeros(int(lib.nb_attention_work_floats(H)), device=dev)
     done = torch.zeros(H, dtype=torch.int32, device=dev)
-    kd, vd = kc.to(dev), vc.to(dev)
+    kd, vd = kc.transpose(1, 2).contiguous().to(dev), vc.to(dev)   # keys [H][D][ctx]
     cosd, sind = cos.to(dev), sin.to(dev)
-    for pos in (0, 1, 15, 16, 17, 63, 79):
+    for pos in sorted({0, 1, 15, 16, 17, 63, ctx // 2, ctx - 1}):
         note(f"attention H={H} D={D} pos={pos}")
         qkv = torch.randn(3 * H * D, generator=g)
         qkvd = qkv.to(dev)
@@ -136,7 +135,7 @@ def test_attention_step(dev, H, D):
                                          P(done), P(out), _lib.NB_F32, H, D, ctx, stream()))
         ref, kc, vc = torch_attention(qkv, kc, vc, pos, H, D, ctx)
         assert rel(out, ref) <= 1e-5, (pos, rel(out, ref))
-        assert torch.allclose(kd.cpu(), kc, rtol=1e-6, atol=1e-6)
+        assert torch.allclose(kd.cpu().transpose(1, 2), kc, rtol=1e-6, atol=1e-6)
         assert torch.equal(vd.cpu(), vc)
         assert int(done.abs().sum()) == 0
 
