@@ -94,6 +94,21 @@ int nb_gemv(const void* x, int x_dtype, int64_t ldx,
             void* stream);
 
 /*
+ * Prefill / batched contraction with a packed weight:
+ *     y[m][n] = sum_k x[m][k] * bf16(W[n][k]),  0 <= m < M, 0 <= n < N,
+ * W a 3-bit stream with 8-entry fp32 codebooks per block of 128 (entries
+ * rounded to bf16 as the reference's bf16 path), x bf16 with row stride ldx
+ * (ldx % 8 == 0, x 16-byte aligned), y NB_BF16 or NB_F32 with row stride
+ * ldy, fp32 accumulation.  Any M, N >= 1; K % 128 == 0.
+ * Replaces: the batched branch of PackedLinear.forward (unpack + gather +
+ *           x @ W.T, inference/triton_kernel.py:258-275) in its bf16 form
+ *           (inference/eval_ppl.py:149-174, compare.py:265-288), and the
+ *           TPU prefill kernel (nativebit_jax/packed_kernel.py:108-178).
+ */
+int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* stream);
+
+/*
  * Unpack `count` indices of `bits` bits to one byte each.
  * Replaces: unpack_3bit / unpack_4bit / unpack_nbits
  *           (nativebit/pack.py:44-68, 85-90, 119-138) and

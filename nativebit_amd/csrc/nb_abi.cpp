@@ -406,3 +406,25 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
 }
 
 }  // extern "C"
+
+extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed,
+                               const float* codebook, void* y, int y_dtype, int64_t ldy, int M,
+                               int N, int K, void* stream) {
+    const char* fn = "nb_gemm_prefill";
+    if (M < 0 || N < 0 || K < 0) return fail(NB_EINVAL, "%s: negative shape", fn);
+    if (K % 128 != 0) return fail(NB_EUNSUPPORTED, "%s: K=%d not a multiple of 128", fn, K);
+    if ((int64_t)N * (K / 128) >= (1LL << 31)) return fail(NB_EUNSUPPORTED, "%s: too many blocks", fn);
+    if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
+    if (M == 0 || N == 0) return NB_OK;
+    if (K == 0) return fail(NB_EUNSUPPORTED, "%s: K == 0 (use nb_gemv)", fn);
+    if (ldx < K || ldy < N) return fail(NB_EINVAL, "%s: ldx=%lld < K or ldy=%lld < N", fn,
+                                        (long long)ldx, (long long)ldy);
+    if (!x || !packed || !codebook || !y) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(x, 16) || ldx % 8 != 0) return fail(NB_EALIGN, "%s: x must be 16-byte aligned with ldx %% 8 == 0", fn);
+    if (!aligned(packed, 8) || !aligned(codebook, 16)) return fail(NB_EALIGN, "%s: packed 8- / codebook 16-byte alignment", fn);
+    if (!aligned(y, dtype_size(y_dtype))) return fail(NB_EALIGN, "%s: y not aligned to its dtype", fn);
+    int st = ensure_device();
+    if (st) return st;
+    return launch_prefill(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
+                          static_cast<hipStream_t>(stream));
+}

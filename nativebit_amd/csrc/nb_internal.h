@@ -88,6 +88,10 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
                    int n_entries, int block_size, hipStream_t stream);
 
 
+// Prefill GEMM with a packed weight (nb_prefill.hip); arguments validated.
+int launch_prefill(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                   void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
 // Decode-step kernels (nb_decode.hip).
 int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
                        const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream);

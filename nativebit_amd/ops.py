@@ -137,6 +137,33 @@ class GemvBatch:
                                                _DT[self.y_dtype], stream))
 
 
+def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
+                 K: int, out_dtype: torch.dtype = torch.bfloat16,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ bf16(W).T for a 3-bit / 8-entry / block-128 packed W (N x K);
+    x (M, K) bfloat16, row-contiguous, fp32 accumulation."""
+    for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
+        _require_cuda(name, t)
+    _same_device(x, packed, codebook)
+    if x.dim() != 2 or x.shape[1] != K or x.dtype != torch.bfloat16 or x.stride(1) != 1:
+        raise ValueError(f"x must be a row-contiguous (M, {K}) bfloat16 tensor")
+    if x.stride(0) % 8 or x.data_ptr() % 16:
+        x = x.contiguous()
+    if codebook.shape != (N * K // 128, 8) or codebook.dtype != torch.float32:
+        raise ValueError("codebook must be (N*K/128, 8) float32")
+    if packed.dtype != torch.uint8 or packed.numel() < packed_nbytes(N * K, 3):
+        raise ValueError("packed must hold the 3-bit stream of N*K indices")
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    elif out.shape != (M, N) or out.dtype not in _DT or out.stride(1) != 1:
+        raise ValueError("out must be (M, N), row-contiguous")
+    _lib.check(_lib.load().nb_gemm_prefill(
+        x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
+        _DT[out.dtype], out.stride(0), M, N, K, _stream(x)))
+    return out
+
+
 def unpack(packed: torch.Tensor, count: int, bits: int) -> torch.Tensor:
     """uint8 indices from an LSB-first stream (device)."""
     _require_cuda("packed", packed)

@@ -1,0 +1,86 @@
+"""GPU parity of the prefill kernel (nb_gemm_prefill, run with -m gpu).
+
+y = x @ bf16(W).T against the fp64 brute force of the oracle on the same
+bf16-rounded codebook entries and bf16 activations (the reference's bf16
+path, inference/eval_ppl.py:149-174): rel <= 1e-3 for fp32 output (fp32
+accumulation), <= 1e-2 for bf16 output; ragged M and N, every 2.2B layer
+shape, and agreement with the batched GEMV on shared rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from nativebit_amd import ops, synth
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def rel(a, b):
+    a = np.asarray(a, dtype=np.float64).reshape(-1)
+    b = np.asarray(b, dtype=np.float64).reshape(-1)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def layer(N, K, seed):
+    rng = np.random.default_rng(seed)
+    nb = N * K // 128
+    idx = rng.integers(0, 8, nb * 128, dtype=np.uint8)
+    cb = (rng.standard_normal((nb, 8)) * 0.02).astype(np.float32)
+    return idx, O.pack(idx, 3), cb
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 128), (200, 300, 384), (1, 100, 128),
+                                   (17, 2560, 2560), (512, 2560, 2560), (300, 7680, 2560),
+                                   (64, 2560, 6912)])
+@pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])
+def test_prefill_vs_f64(dev, M, N, K, ydt):
+    note(f"prefill M={M} N={N} K={K} {ydt}")
+    idx, p, cb = layer(N, K, M * 7 + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + N)).to(torch.bfloat16)
+    xd, pd, cd = x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    y = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=ydt)
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+    w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+    # fp64 brute force on row subsets for the large shapes (keeps the CPU time short)
+    rows = np.arange(M) if M * N * K <= 2e8 else np.unique(np.linspace(0, M - 1, 24).astype(int))
+    ref = O.matmul_f64(x.float().numpy()[rows], w)
+    got = y.float().cpu().numpy()[rows]
+    assert rel(got, ref) <= (1e-3 if ydt == torch.float32 else 1e-2), rel(got, ref)
+
+
+def test_prefill_strided_x_and_out(dev):
+    M, N, K = 96, 256, 512
+    idx, p, cb = layer(N, K, 5)
+    big = torch.randn(M, K + 64).to(torch.bfloat16).to(dev)
+    x = big[:, :K]                      # row stride K + 64 (a multiple of 8)
+    out = torch.full((M, N + 8), float("nan"), device=dev)[:, :N]
+    ops.gemm_prefill(x, torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K,
+                     out=out)
+    w = torch.from_numpy(O.dequant(idx, cb, 128, N * K).reshape(N, K)).to(torch.bfloat16).float()
+    ref = x.float().cpu() @ w.T
+    assert rel(out.cpu(), ref) <= 1e-5
+
+
+def test_prefill_matches_batched_gemv(dev):
+    """Row 0 of a prefill equals the single-token GEMV of the same layer."""
+    lay = synth.make_layer(6912, 2560, seed=11, device=dev)
+    x = synth.make_activation(2560, m=33, seed=12, device=dev, dtype=torch.bfloat16)
+    y = ops.gemm_prefill(x, lay.packed, lay.codebook, 6912, 2560, out_dtype=torch.float32)
+    for m in (0, 17, 32):
+        yv = torch.empty(6912, device=dev)
+        ops.GemvBatch([(x[m].contiguous(), lay.packed, lay.codebook, yv, 6912, 2560)]).run()
+        assert rel(y[m].cpu(), yv.cpu()) <= 1e-5
+
+
+def test_prefill_deterministic(dev):
+    idx, p, cb = layer(2560, 2560, 9)
+    x = torch.randn(256, 2560).to(torch.bfloat16).to(dev)
+    pd, cd = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    a = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32)
+    b = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32)
+    assert torch.equal(a, b)
