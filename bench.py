@@ -18,9 +18,22 @@ same buffers, each captured once in a HIP graph and replayed:
             layer (104 nb_gemv launches; q|k|v and gate|up share x)
 
 `value` is the batched schedule: algorithmic bytes per step / HIP-event time
-per replay.  The other two are reported beside it.
+per replay.  The other two are reported beside it.  The other BASELINE
+configurations are reported in the same JSON line under "configs":
+
+  decode   config 4b: random-init 2.2B packed model (vocab 32000), greedy,
+           128 prompt + 256 generated tokens, tokens/s of the generation
+           (nativebit_amd.decode: one HIP graph per token)
+  prefill  config 4a: nb_gemm_prefill on one layer's matmuls at M = 512 and
+           2048 tokens, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA
+           peak, beside torch's dense bf16 matmul of an unpacked weight
+  skinny   config 2: nb_gemv at M = 1, 2, 4, 8, 16 over all 182 matmuls
+  sweep    config 3: nb_gemv at batch 1, NE in {4, 8, 16} x BS in {64, 128,
+           256} on 6912x2560 and 2560x6912 (random indices and codebooks;
+           copies rotated over > 512 MB so no cache holds them)
 
 Usage: python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--no-extra] [--extra decode,prefill,skinny,sweep]
 """
 from __future__ import annotations
 
@@ -60,6 +73,10 @@ def parse():
     p.add_argument("--cpu-reps", type=int, default=3, help="minimum CPU baseline passes")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline passes continue until this much time has been spent")
+    p.add_argument("--no-extra", action="store_true",
+                   help="skip the decode / prefill / skinny / sweep configurations")
+    p.add_argument("--extra", default="decode,prefill,skinny,sweep",
+                   help="comma list of extra configurations to run")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also time a plain 1 GiB device copy (the yardstick that scales "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -232,6 +249,136 @@ def cpu_baseline(mats, reps, seconds):
     }
 
 
+def event_time(fn, reps, warmup=3):
+    """ms per call of fn() on the current stream (HIP events)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def bench_decode(dev):
+    """Config 4b: greedy decode tokens/s of a random-init 2.2B packed model."""
+    from nativebit_amd.decode import DecodeEngine
+    from nativebit_amd.model import ModelConfig, random_packed_model
+    cfg = ModelConfig(vocab_size=32000)
+    t0 = time.time()
+    model = random_packed_model(cfg, seed=0, device=dev)
+    eng = DecodeEngine(model, max_steps=512)
+    gen = torch.Generator().manual_seed(2024)
+    prompt = torch.randint(0, cfg.vocab_size, (128,), generator=gen).tolist()
+    r = eng.benchmark(prompt, 256, n_runs=3)
+    out = {"tokens_per_s": round(r["generate_tps"], 1), "ms_per_token": round(r["per_token_ms"], 4),
+           "prompt_tokens": 128, "generated_tokens": 256, "vocab": cfg.vocab_size,
+           "runs": r["runs"], "model_build_s": round(time.time() - t0, 1),
+           "method": "median of 3 runs; each: prompt fed (teacher forced), then 255 graph "
+                     "replays timed (the first generated token comes out of the prompt pass)"}
+    del eng, model
+    torch.cuda.empty_cache()
+    return out
+
+
+PREFILL_SHAPES = (("qkv", 7680, 2560), ("o", 2560, 2560), ("gate|up", 13824, 2560),
+                  ("down", 2560, 6912))
+
+
+def bench_prefill(dev):
+    """Config 4a: prefill-sized contraction with the packed weights."""
+    from nativebit_amd import ops, synth
+    layers = {n: synth.make_layer(N, K, seed=50 + i, device=dev)
+              for i, (n, N, K) in enumerate(PREFILL_SHAPES)}
+    out = {}
+    for M in (512, 2048):
+        xs = {K: synth.make_activation(K, m=M, seed=M + K, device=dev, dtype=torch.bfloat16)
+              for K in (2560, 6912)}
+        per, tot_ms, tot_fl, ref_ms = {}, 0.0, 0, 0.0
+        for n, N, K in PREFILL_SHAPES:
+            lay = layers[n]
+            y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+            ms = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y), 20)
+            w = torch.empty(N, K, dtype=torch.bfloat16, device=dev).normal_()
+            ms_ref = event_time(lambda: torch.matmul(xs[K], w.T), 20)
+            fl = 2 * M * N * K
+            per[n] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / ms / 1e9, 1),
+                      "torch_dense_bf16_us": round(ms_ref * 1e3, 1)}
+            tot_ms += ms
+            ref_ms += ms_ref
+            tot_fl += fl
+            del w
+        out[f"M{M}"] = {"layer_us": round(tot_ms * 1e3, 1),
+                        "TFLOP_s": round(tot_fl / tot_ms / 1e9, 1),
+                        "pct_bf16_mfma_peak": round(tot_fl / tot_ms / 1e9 / 2500 * 100, 2),
+                        "model_26_layers_ms": round(26 * tot_ms, 3),
+                        "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
+                        "per_matmul": per}
+    out["note"] = ("nb_gemm_prefill reads the 3-bit stream and codebooks directly; torch_dense_bf16 "
+                   "is torch.matmul on an already-unpacked bf16 weight (the reference's path also "
+                   "unpacks and gathers W on every call, triton_kernel.py:258-275)")
+    return out
+
+
+def bench_skinny(dev, layers):
+    """Config 2: nb_gemv at M rows over all 182 matmuls (graph of launches)."""
+    from nativebit_amd import ops, synth
+    mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
+    out = {}
+    for M in (1, 2, 4, 8, 16):
+        xs = {K: synth.make_activation(K, m=M, seed=M, device=dev, dtype=torch.bfloat16)
+              for K in (2560, 6912)}
+        ys = [torch.empty(M, m.N, device=dev) for m in mats]
+
+        def run():
+            for m, y in zip(mats, ys):
+                ops.gemv(xs[m.K], m.packed, m.cb, m.N, m.K, out=y)
+        ms = graph_time(run, 20, 5)
+        nbytes = sum(synth.layer_bytes(m.N, m.K, NE, BS, M, 2, 4) for m in mats)
+        fl = 2 * M * sum(m.N * m.K for m in mats)
+        out[f"M{M}"] = {"us_per_step": round(ms * 1e3, 1), "GB_s": round(nbytes / ms / 1e6, 1),
+                        "TFLOP_s": round(fl / ms / 1e9, 2)}
+        del ys, xs
+    out["note"] = "182 nb_gemv launches per step (one per matmul), replayed as one HIP graph"
+    return out
+
+
+def bench_sweep(dev):
+    """Config 3: bit width x block size at batch 1 (nb_gemv)."""
+    from nativebit_amd import ops, synth
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(7)
+    for (N, K) in ((6912, 2560), (2560, 6912)):
+        x = synth.make_activation(K, seed=K, device=dev, dtype=torch.bfloat16)[0].contiguous()
+        for ne in (4, 8, 16):
+            bits = {4: 2, 8: 3, 16: 4}[ne]
+            for bs in (64, 128, 256):
+                per = synth.layer_bytes(N, K, ne, bs, 1, 2, 4)
+                copies = max(2, -(-(512 << 20) // per))
+                nb = N * K // bs
+                from nativebit_amd import pack as host_pack
+                pbytes = host_pack.packed_nbytes(nb * bs, bits)
+                ps = [torch.randint(0, 256, (pbytes,), dtype=torch.uint8, device=dev, generator=gen)
+                      for _ in range(copies)]
+                cbs = [torch.randn(nb, ne, device=dev, generator=gen) * 0.02 for _ in range(copies)]
+                y = torch.empty(1, N, device=dev)
+
+                def run():
+                    for p, c in zip(ps, cbs):
+                        ops.gemv(x, p, c, N, K, bits=bits, block_size=bs, out=y)
+                ms = graph_time(run, 10, 3) / copies
+                out[f"{N}x{K}_NE{ne}_BS{bs}"] = {"us": round(ms * 1e3, 2),
+                                                 "GB_s": round(per / ms / 1e6, 1),
+                                                 "bytes": per, "copies": copies}
+                del ps, cbs
+    out["note"] = ("batch-1 nb_gemv, bf16 x, fp32 y; each timed launch reads a different copy "
+                   "(copies x bytes > 512 MB); random indices and codebooks")
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -333,6 +480,21 @@ def main():
         "schedules": results,
         "parity": {"spot_check_rel_err_vs_f64": err},
     }
+    if not args.no_extra:
+        extra = {}
+        wanted_extra = [e for e in args.extra.split(",") if e]
+        for name, fn in (("decode", lambda: bench_decode(dev)),
+                         ("prefill", lambda: bench_prefill(dev)),
+                         ("skinny", lambda: bench_skinny(dev, layers)),
+                         ("sweep", lambda: bench_sweep(dev))):
+            if name not in wanted_extra:
+                continue
+            t0 = time.time()
+            log(f"[bench] {name} ...")
+            extra[name] = fn()
+            log(f"[bench] {name} done in {time.time() - t0:.1f}s: "
+                f"{json.dumps(extra[name])[:300]}")
+        result["configs"] = extra
     if args.copy_calibration:
         result["copy_calibration"] = copy_calibration(dev, args.steps, args.warmup)
         log(f"[bench] copy calibration: {result['copy_calibration']}")
