@@ -157,3 +157,88 @@ def test_batch_validation():
     assert lib.nb_gemv_batched(arr, FAKE, 2, 7, None) == _lib.NB_EINVAL
     empty = (Item * 1)(Item(None, None, None, None, 0, 256))
     assert lib.nb_gemv_batched(empty, None, 1, _lib.NB_F32, None) == _lib.NB_OK
+
+
+# --- prefill and decode-step entry points: host-side validation -------------
+
+def prefill(**kw):
+    a = dict(x=FAKE, ldx=256, packed=FAKE, codebook=FAKE, y=FAKE, y_dtype=_lib.NB_BF16, ldy=64,
+             M=32, N=64, K=256, stream=None)
+    a.update(kw)
+    return _lib.load().nb_gemm_prefill(*a.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=200), _lib.NB_EUNSUPPORTED),
+    (dict(M=-1), _lib.NB_EINVAL),
+    (dict(ldx=128), _lib.NB_EINVAL),
+    (dict(ldy=10), _lib.NB_EINVAL),
+    (dict(y_dtype=7), _lib.NB_EINVAL),
+    (dict(x=None), _lib.NB_EINVAL),
+    (dict(x=FAKE + 8), _lib.NB_EALIGN),
+    (dict(ldx=260), _lib.NB_EALIGN),
+    (dict(codebook=FAKE + 4), _lib.NB_EALIGN),
+])
+def test_prefill_validation(kw, status):
+    assert prefill(**kw) == status
+    assert _lib.last_error().startswith("nb_gemm_prefill")
+
+
+def test_prefill_empty_is_ok():
+    assert prefill(M=0) == _lib.NB_OK and prefill(N=0) == _lib.NB_OK
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(n=0), _lib.NB_EINVAL),
+    (dict(h_dtype=5), _lib.NB_EINVAL),
+    (dict(emb=FAKE, state=None), _lib.NB_EINVAL),
+    (dict(x=None), _lib.NB_EINVAL),
+    (dict(eps=-1.0), _lib.NB_EINVAL),
+    (dict(w=FAKE + 2), _lib.NB_EALIGN),
+])
+def test_add_rmsnorm_validation(kw, status):
+    a = dict(x=FAKE, y=None, emb=None, state=FAKE, w=FAKE, h=FAKE, h_dtype=_lib.NB_BF16, n=2560,
+             eps=1e-6, stream=None)
+    a.update(kw)
+    assert _lib.load().nb_add_rmsnorm(*a.values()) == status
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(head_dim=127), _lib.NB_EUNSUPPORTED),
+    (dict(head_dim=512), _lib.NB_EUNSUPPORTED),
+    (dict(ctx=2048), _lib.NB_EUNSUPPORTED),
+    (dict(n_head=0), _lib.NB_EINVAL),
+    (dict(work=None), _lib.NB_EINVAL),
+    (dict(out_dtype=9), _lib.NB_EINVAL),
+    (dict(k_cache=FAKE + 2), _lib.NB_EALIGN),
+])
+def test_attention_step_validation(kw, status):
+    a = dict(qkv=FAKE, k_cache=FAKE, v_cache=FAKE, cos=FAKE, sin=FAKE, state=FAKE, work=FAKE,
+             done=FAKE, out=FAKE, out_dtype=_lib.NB_BF16, n_head=20, head_dim=128, ctx=1024,
+             stream=None)
+    a.update(kw)
+    assert _lib.load().nb_attention_step(*a.values()) == status
+    assert _lib.load().nb_attention_work_floats(20) > 20 * 128
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(C=100), _lib.NB_EUNSUPPORTED),
+    (dict(C=16384), _lib.NB_EUNSUPPORTED),
+    (dict(V=0), _lib.NB_EUNSUPPORTED),
+    (dict(n_force=3, force=None), _lib.NB_EINVAL),
+    (dict(tokens_cap=4, tokens=None), _lib.NB_EINVAL),
+    (dict(state=None), _lib.NB_EINVAL),
+    (dict(emb=FAKE + 8), _lib.NB_EALIGN),
+])
+def test_lm_head_validation(kw, status):
+    a = dict(h=FAKE, emb=FAKE, logits=None, state=FAKE, tokens=None, tokens_cap=0, force=None,
+             n_force=0, V=32000, C=2560, stream=None)
+    a.update(kw)
+    assert _lib.load().nb_lm_head_argmax(*a.values()) == status
+
+
+def test_silu_mul_validation():
+    lib = _lib.load()
+    assert lib.nb_silu_mul(FAKE, FAKE, _lib.NB_BF16, 0, None) == _lib.NB_EINVAL
+    assert lib.nb_silu_mul(None, FAKE, _lib.NB_BF16, 8, None) == _lib.NB_EINVAL
+    assert lib.nb_silu_mul(FAKE, FAKE, 3, 8, None) == _lib.NB_EINVAL
