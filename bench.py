@@ -264,7 +264,8 @@ def event_time(fn, reps, warmup=3):
 
 
 def bench_decode(dev):
-    """Config 4b: greedy decode tokens/s of a random-init 2.2B packed model."""
+    """Config 4b: greedy decode tokens/s of a random-init 2.2B packed model
+    (one HIP graph of launches replayed per token)."""
     from nativebit_amd.decode import DecodeEngine
     from nativebit_amd.model import ModelConfig, random_packed_model
     cfg = ModelConfig(vocab_size=32000)
@@ -277,6 +278,7 @@ def bench_decode(dev):
     out = {"tokens_per_s": round(r["generate_tps"], 1), "ms_per_token": round(r["per_token_ms"], 4),
            "prompt_tokens": 128, "generated_tokens": 256, "vocab": cfg.vocab_size,
            "runs": r["runs"], "model_build_s": round(time.time() - t0, 1),
+           "engine": "DecodeEngine: one HIP graph of the step's launches, replayed per token",
            "method": "median of 3 runs; each: prompt fed (teacher forced), then 255 graph "
                      "replays timed (the first generated token comes out of the prompt pass)"}
     del eng, model

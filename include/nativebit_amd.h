@@ -251,8 +251,64 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
                       int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                       int V, int C, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Persistent decode: many greedy tokens of the whole packed decoder in one
+ * cooperative launch (one workgroup per CU), the phases of a token separated
+ * by grid barriers instead of kernel boundaries, and the packed weights of
+ * the next phases streamed while a phase waits.
+ * ------------------------------------------------------------------------ */
+/* The packed matmuls, norms and caches of one decoder layer (device
+ * pointers).  Streams are 3-bit with 8-entry fp32 codebooks per block of 128
+ * (the format above), 16-byte aligned.  q|k|v and gate|up are fused by rows:
+ * qkv is the q, k and v weights stacked (3C x C, the reference's fused qkv,
+ * inference/generate_torch.py:68), gu the gate then the up weights (2F x C). */
+typedef struct nb_decode_layer {
+    const uint8_t* qkv_packed;   const float* qkv_codebook;   /* 3C x C          */
+    const uint8_t* o_packed;     const float* o_codebook;     /* C x C           */
+    const uint8_t* gu_packed;    const float* gu_codebook;    /* 2F x C          */
+    const uint8_t* down_packed;  const float* down_codebook;  /* C x F           */
+    const float* ln1;            const float* ln2;            /* C fp32 each     */
+    float* k_cache;                                           /* [H][D][ctx] fp32 */
+    float* v_cache;                                           /* [H][ctx][D] fp32 */
+} nb_decode_layer;
+typedef struct nb_decode_model {
+    int32_t n_layers, n_embd, n_head, head_dim, ffn_hidden, vocab, ctx;
+    float eps;                       /* RMSNorm epsilon                        */
+    const nb_decode_layer* layers;   /* device array of n_layers entries       */
+    const float* ln_f;               /* final norm weight, n_embd fp32         */
+    const float* emb_f32;            /* [vocab][n_embd] fp32 (token lookup)    */
+    const void* emb_bf16;            /* [vocab][n_embd] bf16 (tied head)       */
+    const float* rope_cos;           /* [ctx][head_dim / 2] fp32               */
+    const float* rope_sin;
+} nb_decode_model;
+/* Byte offset, inside the workspace, of a uint32 that is 0 after a call that
+ * completed and 1 after one whose grid barrier wait ran past the spin limit
+ * (its outputs are then invalid). */
+#define NB_DECODE_ERR_OFFSET 2304
+/* Workspace bytes nb_decode_persistent needs for this model (0 if the
+ * shapes are outside its limits; nb_last_error says why). */
+int64_t nb_decode_workspace_bytes(const nb_decode_model* model);
+/*
+ * Feeds state->token at state->pos and runs n_steps greedy steps -- the same
+ * model and the same state updates as n_steps of nb_add_rmsnorm ...
+ * nb_lm_head_argmax per layer (forced tokens, tokens_out, pos and step
+ * advance) -- in one launch.  logits (may be NULL) receives the last step's
+ * capped logits.  The workspace (256-byte aligned, caller-owned device
+ * memory) holds activations and barrier counters; the call clears its
+ * control block.  Limits: n_embd and ffn_hidden multiples of 128, n_embd <=
+ * 4096, ffn_hidden <= 8192, head_dim even and <= 128, ctx <= 1024, and
+ * every layer large enough to give each CU a chunk of rows.  state->pos +
+ * n_steps must not exceed ctx.  spin_limit bounds each grid barrier wait
+ * (polls of about 100 ns; <= 0 selects 2^20).
+ * Replaces: the token loop of PackedGPT generation (inference/
+ *           generate_torch.py:135-162, 298-313) with its packed linears
+ *           (inference/triton_kernel.py:223-286).
+ */
+int nb_decode_persistent(const nb_decode_model* model, void* workspace, int64_t workspace_bytes,
+                         nb_decode_state* state, float* logits, int32_t* tokens_out,
+                         int tokens_cap, const int32_t* force, int n_force, int n_steps,
+                         int spin_limit, void* stream);
 #ifdef __cplusplus
 }
 #endif
-
 #endif /* NATIVEBIT_AMD_H */

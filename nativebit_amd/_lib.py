@@ -56,7 +56,12 @@ SIGNATURES = {
     "nb_attention_work_floats": (_I, [_I]),
     "nb_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "nb_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
+    "nb_decode_workspace_bytes": (_L, [_P]),
+    "nb_decode_persistent": (_I, [_P, _P, _L, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
 }
+
+# Byte offset of the persistent decode's error word in its workspace.
+NB_DECODE_ERR_OFFSET = 2304
 
 
 class BatchItem(ctypes.Structure):
@@ -70,6 +75,24 @@ class DecodeState(ctypes.Structure):
     """struct nb_decode_state (include/nativebit_amd.h)."""
     _fields_ = [("key", ctypes.c_uint64), ("pos", ctypes.c_int32), ("token", ctypes.c_int32),
                 ("step", ctypes.c_int32), ("done", ctypes.c_uint32)]
+
+
+class DecodeLayer(ctypes.Structure):
+    """struct nb_decode_layer (include/nativebit_amd.h): device pointers."""
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "qkv_packed", "qkv_codebook", "o_packed", "o_codebook", "gu_packed", "gu_codebook",
+        "down_packed", "down_codebook", "ln1", "ln2", "k_cache", "v_cache")]
+
+
+class DecodeModel(ctypes.Structure):
+    """struct nb_decode_model (include/nativebit_amd.h)."""
+    _fields_ = [("n_layers", ctypes.c_int32), ("n_embd", ctypes.c_int32),
+                ("n_head", ctypes.c_int32), ("head_dim", ctypes.c_int32),
+                ("ffn_hidden", ctypes.c_int32), ("vocab", ctypes.c_int32),
+                ("ctx", ctypes.c_int32), ("eps", ctypes.c_float),
+                ("layers", ctypes.c_void_p), ("ln_f", ctypes.c_void_p),
+                ("emb_f32", ctypes.c_void_p), ("emb_bf16", ctypes.c_void_p),
+                ("rope_cos", ctypes.c_void_p), ("rope_sin", ctypes.c_void_p)]
 
 
 class NativeBitError(RuntimeError):

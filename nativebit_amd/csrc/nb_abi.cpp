@@ -428,3 +428,75 @@ extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed
     return launch_prefill(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
                           static_cast<hipStream_t>(stream));
 }
+
+namespace {
+// Shapes and pointers of a persistent-decode model; NB_OK or a status.
+int check_decode_model(const nb_decode_model* m, const char* fn) {
+    if (!m) return fail(NB_EINVAL, "%s: NULL model", fn);
+    int max_c, max_f, max_d, max_ctx, max_heads, max_layers;
+    decode_persistent_limits(&max_c, &max_f, &max_d, &max_ctx, &max_heads, &max_layers);
+    if (m->n_layers < 1 || m->n_embd < 1 || m->n_head < 1 || m->head_dim < 1 ||
+        m->ffn_hidden < 1 || m->vocab < 1 || m->ctx < 1) {
+        return fail(NB_EINVAL, "%s: non-positive model dimension", fn);
+    }
+    if (m->n_layers > max_layers) {
+        return fail(NB_EUNSUPPORTED, "%s: n_layers=%d > %d", fn, m->n_layers, max_layers);
+    }
+    if (m->n_embd % 128 || m->ffn_hidden % 128 || m->n_embd > max_c || m->ffn_hidden > max_f) {
+        return fail(NB_EUNSUPPORTED, "%s: n_embd=%d / ffn_hidden=%d (multiples of 128, <= %d / %d)",
+                    fn, m->n_embd, m->ffn_hidden, max_c, max_f);
+    }
+    if (m->head_dim % 2 || m->head_dim > max_d || (int64_t)m->n_head * m->head_dim != m->n_embd ||
+        m->n_head > max_heads) {
+        return fail(NB_EUNSUPPORTED, "%s: n_head=%d head_dim=%d (even head_dim <= %d, "
+                    "n_head * head_dim == n_embd, n_head <= %d)", fn, m->n_head, m->head_dim,
+                    max_d, max_heads);
+    }
+    if (m->ctx > max_ctx) return fail(NB_EUNSUPPORTED, "%s: ctx=%d > %d", fn, m->ctx, max_ctx);
+    if (!(m->eps >= 0.f)) return fail(NB_EINVAL, "%s: eps must be >= 0", fn);
+    if (!m->layers || !m->ln_f || !m->emb_f32 || !m->emb_bf16 || !m->rope_cos || !m->rope_sin) {
+        return fail(NB_EINVAL, "%s: NULL model pointer", fn);
+    }
+    if (!aligned(m->layers, 8) || !aligned(m->ln_f, 4) || !aligned(m->emb_f32, 4) ||
+        !aligned(m->emb_bf16, 16) || !aligned(m->rope_cos, 4) || !aligned(m->rope_sin, 4)) {
+        return fail(NB_EALIGN, "%s: misaligned model pointer", fn);
+    }
+    return NB_OK;
+}
+}  // namespace
+
+extern "C" int64_t nb_decode_workspace_bytes(const nb_decode_model* model) {
+    if (check_decode_model(model, "nb_decode_workspace_bytes")) return 0;
+    return decode_persistent_workspace_bytes(model->n_embd, model->n_head, model->ffn_hidden);
+}
+
+extern "C" int nb_decode_persistent(const nb_decode_model* model, void* workspace,
+                                    int64_t workspace_bytes, nb_decode_state* state, float* logits,
+                                    int32_t* tokens_out, int tokens_cap, const int32_t* force,
+                                    int n_force, int n_steps, int spin_limit, void* stream) {
+    const char* fn = "nb_decode_persistent";
+    int st = check_decode_model(model, fn);
+    if (st) return st;
+    if (n_steps < 0) return fail(NB_EINVAL, "%s: n_steps=%d < 0", fn, n_steps);
+    if (!workspace || !state) return fail(NB_EINVAL, "%s: NULL workspace or state", fn);
+    const int64_t need = decode_persistent_workspace_bytes(model->n_embd, model->n_head,
+                                                           model->ffn_hidden);
+    if (workspace_bytes < need) {
+        return fail(NB_EINVAL, "%s: workspace of %lld bytes, %lld needed", fn,
+                    (long long)workspace_bytes, (long long)need);
+    }
+    if (n_force < 0 || (n_force > 0 && !force)) return fail(NB_EINVAL, "%s: n_force=%d without force", fn, n_force);
+    if (tokens_cap < 0 || (tokens_cap > 0 && !tokens_out)) {
+        return fail(NB_EINVAL, "%s: tokens_cap=%d without tokens_out", fn, tokens_cap);
+    }
+    if (!aligned(workspace, 256) || !aligned(state, 8) || (logits && !aligned(logits, 4)) ||
+        (tokens_out && !aligned(tokens_out, 4)) || (force && !aligned(force, 4))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer (workspace needs 256 bytes)", fn);
+    }
+    if (n_steps == 0) return NB_OK;
+    st = ensure_device();
+    if (st) return st;
+    return launch_decode_persistent(*model, workspace, state, logits, tokens_out, tokens_cap, force,
+                                    n_force, n_steps, spin_limit > 0 ? spin_limit : (1 << 20),
+                                    static_cast<hipStream_t>(stream));
+}

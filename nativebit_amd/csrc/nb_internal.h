@@ -104,6 +104,15 @@ int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_deco
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                           int V, int C, hipStream_t stream);
 int attention_work_floats(int n_head);
+
+// Persistent decode (nb_decode_persistent.hip); arguments validated.
+int64_t decode_persistent_workspace_bytes(int C, int H, int F);
+int decode_persistent_limits(int* max_c, int* max_f, int* max_d, int* max_ctx, int* max_heads,
+                             int* max_layers);
+int launch_decode_persistent(const nb_decode_model& m, void* workspace, nb_decode_state* st,
+                             float* logits, int32_t* tokens_out, int tokens_cap,
+                             const int32_t* force, int n_force, int n_steps, int spin_limit,
+                             hipStream_t stream);
 int attention_max_head_dim();
 int attention_max_ctx();
 int lm_head_max_c();

@@ -1,13 +1,17 @@
-"""Greedy decode of a packed NativeBit model as one HIP graph per token.
+"""Greedy decode of a packed NativeBit model on the GPU, two ways.
 
-The same model as ``nativebit_amd.model.PackedGPT`` (inference/
-generate_torch.py:135-162), run as a fixed sequence of gfx950 launches per
-token: per layer nb_add_rmsnorm -> q|k|v GEMV -> nb_attention_step -> o
-GEMV -> nb_add_rmsnorm -> gate|up GEMV -> nb_silu_mul -> down GEMV, then the
-final norm and nb_lm_head_argmax.  The position and the current token live
-in device memory, so the step is captured once in a HIP graph and replayed
-per token with no host round trip (the reference synchronises on
-``int(logits.argmax())`` every token, generate_torch.py:311).
+Both run the model of ``nativebit_amd.model.PackedGPT`` (inference/
+generate_torch.py:135-162) with the position and the current token in
+device memory, so no token needs a host round trip (the reference
+synchronises on ``int(logits.argmax())`` every token, generate_torch.py:311).
+
+* ``DecodeEngine``: a token is a fixed sequence of gfx950 launches -- per
+  layer nb_add_rmsnorm -> q|k|v GEMV -> nb_attention_step -> o GEMV ->
+  nb_add_rmsnorm -> gate|up GEMV -> nb_silu_mul -> down GEMV, then the final
+  norm and nb_lm_head_argmax -- captured once in a HIP graph and replayed.
+* ``PersistentDecodeEngine``: nb_decode_persistent runs many tokens in one
+  cooperative launch, the phases of a token separated by grid barriers and
+  the packed weights of the next phases streamed during each barrier.
 
 Numerics: the residual stream, norms, attention and KV cache are fp32 as in
 the reference; the activations handed to the packed GEMVs are rounded to
@@ -39,14 +43,16 @@ def _fuse_rows(layers):
     return packed, cb, sum(l.out_features for l in layers), layers[0].in_features
 
 
-class DecodeEngine:
-    """Device-resident greedy decoder for one sequence (batch 1)."""
+class _DecoderBase:
+    """Device-resident state shared by the decode engines: fused weights,
+    norms, caches, embedding copies, the decode state, forced and chosen
+    tokens, and the whole-sequence API."""
 
     def __init__(self, model: PackedGPT, max_steps: int | None = None):
         cfg = model.cfg
         dev = model.embedding.weight.device
         if dev.type != "cuda":
-            raise ValueError("DecodeEngine runs on a ROCm GPU")
+            raise ValueError(f"{type(self).__name__} runs on a ROCm GPU")
         self.model, self.cfg, self.dev = model, cfg, dev
         C, F, H = cfg.n_embd, cfg.ffn_hidden, cfg.n_head
         D = C // H
@@ -55,15 +61,8 @@ class DecodeEngine:
         self.ctx = cfg.context_len
         self.max_steps = max_steps or cfg.context_len
         f32, bf16 = torch.float32, torch.bfloat16
-        z = lambda *s, dt=f32: torch.zeros(*s, dtype=dt, device=dev)  # noqa: E731
-        self.x = z(C)
-        self.h = z(C, dt=bf16)
-        self.qkv = z(3 * C)
-        self.att = z(C, dt=bf16)
-        self.o = z(C)
-        self.gu = z(2 * F)
-        self.act = z(F, dt=bf16)
-        self.d = z(C)
+        self._z = lambda *s, dt=f32: torch.zeros(*s, dtype=dt, device=dev)  # noqa: E731
+        z = self._z
         self.logits = z(self.V)
         self.emb_f32 = model.embedding.weight.detach().to(f32).contiguous()
         self.emb_bf16 = self.emb_f32.to(bf16).contiguous()
@@ -71,32 +70,24 @@ class DecodeEngine:
         self.cos, self.sin = cos.to(dev).contiguous(), sin.to(dev).contiguous()
         self.kc = z(cfg.n_layers, H, D, self.ctx)   # keys transposed: [layer][head][dim][pos]
         self.vc = z(cfg.n_layers, H, self.ctx, D)
-        lib = _lib.load()
-        self.work = z(int(lib.nb_attention_work_floats(H)))
-        self.done = z(H, dt=torch.int32)
         self.state_t = z(32, dt=torch.uint8)
         self.tokens = z(self.max_steps, dt=torch.int32)
         self.force = z(self.max_steps, dt=torch.int32)
         self.n_force = 0
+        # per layer: fused q|k|v and gate|up streams (rows never share a
+        # block, so the fused stream is the layers' streams concatenated)
+        self.fused = []
         self.norms = []
-        self.gemvs = []
-        self._keep = []
         for blk in model.blocks:
-            qkv_p, qkv_c, qkv_n, _ = _fuse_rows([blk.attn.qkv])
-            gu_p, gu_c, gu_n, _ = _fuse_rows([blk.ffn.gate, blk.ffn.up])
-            self._keep += [gu_p, gu_c]
+            qkv_p, qkv_c, _, _ = _fuse_rows([blk.attn.qkv])
+            gu_p, gu_c, _, _ = _fuse_rows([blk.ffn.gate, blk.ffn.up])
             o, dn = blk.attn.out_proj, blk.ffn.down
-            self.gemvs.append((
-                ops.GemvBatch([(self.h, qkv_p, qkv_c, self.qkv, qkv_n, C)]),
-                ops.GemvBatch([(self.att, o.packed_indices, o.codebook, self.o, C, C)]),
-                ops.GemvBatch([(self.h, gu_p, gu_c, self.gu, 2 * F, C)]),
-                ops.GemvBatch([(self.act, dn.packed_indices, dn.codebook, self.d, C, F)]),
-            ))
+            self.fused.append(((qkv_p, qkv_c), (o.packed_indices, o.codebook), (gu_p, gu_c),
+                               (dn.packed_indices, dn.codebook)))
             self.norms.append((blk.ln1.weight.detach().float().contiguous(),
                                blk.ln2.weight.detach().float().contiguous()))
         self.ln_f = model.ln_f.weight.detach().float().contiguous()
         self.eps = float(cfg.norm_eps)
-        self.graph = None
         self.fed = 0
 
     # -- state ------------------------------------------------------------
@@ -118,11 +109,90 @@ class DecodeEngine:
             self.force[: self.n_force].copy_(torch.tensor(prompt[1:], dtype=torch.int32))
         self.kc.zero_()
         self.vc.zero_()
-        self.done.zero_()
         self.fed = 0
+
+    def _advance(self, n):
+        if self.fed + n > min(self.ctx, self.max_steps):
+            raise ValueError(f"{self.fed} + {n} steps exceed the context ({self.ctx}) or "
+                             f"max_steps ({self.max_steps})")
+        self.fed += n
+
+    def state(self) -> dict:
+        st = _lib.DecodeState.from_buffer_copy(bytes(self.state_t[:24].cpu().numpy()))
+        return {"pos": st.pos, "token": st.token, "step": st.step, "key": st.key, "done": st.done}
+
+    def run(self, n_steps: int):
+        raise NotImplementedError
+
+    def _prepare_timing(self):
+        """Work done once per timed run before the clock starts."""
+
+    # -- whole sequences ----------------------------------------------------
+    @torch.no_grad()
+    def generate(self, prompt_tokens, n_generate: int) -> list:
+        """Greedy continuation: the n_generate tokens the reference's loop
+        produces (generate_torch.py:298-313)."""
+        n_prompt = len(prompt_tokens)
+        if n_prompt + n_generate > min(self.ctx, self.max_steps):
+            raise ValueError("prompt + generated tokens exceed the context")
+        self.reset(prompt_tokens)
+        self.run(n_prompt + n_generate - 1)
+        torch.cuda.synchronize()
+        return self.tokens[n_prompt - 1: n_prompt - 1 + n_generate].cpu().tolist()
+
+    @torch.no_grad()
+    def benchmark(self, prompt_tokens, n_generate: int, n_runs: int = 3) -> dict:
+        """Decode tokens/s after the prompt (timed like generate_torch.py:
+        280-320: the prompt is fed first, then the continuation is timed)."""
+        n_prompt = len(prompt_tokens)
+        times = []
+        for _ in range(n_runs):
+            self.reset(prompt_tokens)
+            self._prepare_timing()
+            self.run(n_prompt)          # prompt (teacher forced) + first token chosen
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            self.run(n_generate - 1)    # the rest of the continuation
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        return {"generate_tps": (n_generate - 1) / t, "per_token_ms": t / (n_generate - 1) * 1e3,
+                "runs": len(times)}
+
+
+class DecodeEngine(_DecoderBase):
+    """Device-resident greedy decoder for one sequence (batch 1): one HIP
+    graph of launches per token."""
+
+    def __init__(self, model: PackedGPT, max_steps: int | None = None):
+        super().__init__(model, max_steps)
+        C, F, H = self.C, self.F, self.H
+        z, bf16 = self._z, torch.bfloat16
+        self.x = z(C)
+        self.h = z(C, dt=bf16)
+        self.qkv = z(3 * C)
+        self.att = z(C, dt=bf16)
+        self.o = z(C)
+        self.gu = z(2 * F)
+        self.act = z(F, dt=bf16)
+        self.d = z(C)
+        self.work = z(int(_lib.load().nb_attention_work_floats(H)))
+        self.done = z(H, dt=torch.int32)
+        self.gemvs = []
+        for (qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c) in self.fused:
+            self.gemvs.append((
+                ops.GemvBatch([(self.h, qkv_p, qkv_c, self.qkv, 3 * C, C)]),
+                ops.GemvBatch([(self.att, o_p, o_c, self.o, C, C)]),
+                ops.GemvBatch([(self.h, gu_p, gu_c, self.gu, 2 * F, C)]),
+                ops.GemvBatch([(self.act, d_p, d_c, self.d, C, F)]),
+            ))
+        self.graph = None
+
+    def reset(self, prompt_tokens):
+        super().reset(prompt_tokens)
+        self.done.zero_()
         self.graph = None  # n_force is baked into the launch
 
-    # -- one step ---------------------------------------------------------
     def _launch(self):
         lib = _lib.load()
         s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
@@ -155,12 +225,6 @@ class DecodeEngine:
                                  _ptr(self.tokens), self.max_steps, _ptr(self.force), self.n_force,
                                  self.V, C, s))
 
-    def _advance(self, n):
-        if self.fed + n > min(self.ctx, self.max_steps):
-            raise ValueError(f"{self.fed} + {n} steps exceed the context ({self.ctx}) or "
-                             f"max_steps ({self.max_steps})")
-        self.fed += n
-
     def step(self):
         """Feed the current token (eagerly, no graph)."""
         self._advance(1)
@@ -169,10 +233,12 @@ class DecodeEngine:
     def capture(self):
         """Capture one step in a HIP graph (replayed by run())."""
         g = torch.cuda.CUDAGraph()
-        # the graph records the launches only; warm the libraries first
         with torch.cuda.graph(g):
             self._launch()
         self.graph = g
+
+    def _prepare_timing(self):
+        self.capture()
 
     def run(self, n_steps: int):
         self._advance(n_steps)
@@ -181,40 +247,55 @@ class DecodeEngine:
         for _ in range(n_steps):
             self.graph.replay()
 
-    def state(self) -> dict:
-        st = _lib.DecodeState.from_buffer_copy(bytes(self.state_t[:24].cpu().numpy()))
-        return {"pos": st.pos, "token": st.token, "step": st.step, "key": st.key, "done": st.done}
 
-    # -- whole sequences ----------------------------------------------------
+class PersistentDecodeEngine(_DecoderBase):
+    """Device-resident greedy decoder for one sequence (batch 1): any number
+    of tokens per launch of nb_decode_persistent."""
+
+    def __init__(self, model: PackedGPT, max_steps: int | None = None, spin_limit: int = 0):
+        super().__init__(model, max_steps)
+        self.spin_limit = int(spin_limit)
+        rows = []
+        for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
+            ln1, ln2 = self.norms[l]
+            rows.append([t.data_ptr() for t in (qkv_p, qkv_c, o_p, o_c, gu_p, gu_c, d_p, d_c,
+                                                ln1, ln2, self.kc[l], self.vc[l])])
+        # the device table of struct nb_decode_layer (12 pointers per layer)
+        self.layer_table = torch.tensor(rows, dtype=torch.int64).to(self.dev)
+        self.desc = _lib.DecodeModel(
+            self.cfg.n_layers, self.C, self.H, self.D, self.F, self.V, self.ctx, self.eps,
+            self.layer_table.data_ptr(), self.ln_f.data_ptr(), self.emb_f32.data_ptr(),
+            self.emb_bf16.data_ptr(), self.cos.data_ptr(), self.sin.data_ptr())
+        lib = _lib.load()
+        nbytes = int(lib.nb_decode_workspace_bytes(ctypes.byref(self.desc)))
+        if nbytes <= 0:
+            raise _lib.NativeBitError(_lib.NB_EUNSUPPORTED, _lib.last_error())
+        self.workspace = self._z(nbytes, dt=torch.uint8)
+
+    def run(self, n_steps: int):
+        """Feed n_steps tokens in one launch (no synchronisation)."""
+        if n_steps <= 0:
+            return
+        self._advance(n_steps)
+        s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        _lib.check(_lib.load().nb_decode_persistent(
+            ctypes.byref(self.desc), _ptr(self.workspace), self.workspace.numel(),
+            _ptr(self.state_t), _ptr(self.logits), _ptr(self.tokens), self.max_steps,
+            _ptr(self.force), self.n_force, n_steps, self.spin_limit, s))
+
+    def step(self):
+        self.run(1)
+
+    def error(self) -> int:
+        """The launch's error word (synchronises): 0, or 1 when a grid
+        barrier wait ran past the spin limit."""
+        off = _lib.NB_DECODE_ERR_OFFSET
+        return int(self.workspace[off: off + 4].view(torch.int32).item())
+
     @torch.no_grad()
     def generate(self, prompt_tokens, n_generate: int) -> list:
-        """Greedy continuation: the n_generate tokens the reference's loop
-        produces (generate_torch.py:298-313)."""
-        n_prompt = len(prompt_tokens)
-        if n_prompt + n_generate > min(self.ctx, self.max_steps):
-            raise ValueError("prompt + generated tokens exceed the context")
-        self.reset(prompt_tokens)
-        self.run(n_prompt + n_generate - 1)
-        torch.cuda.synchronize()
-        return self.tokens[n_prompt - 1: n_prompt - 1 + n_generate].cpu().tolist()
-
-    @torch.no_grad()
-    def benchmark(self, prompt_tokens, n_generate: int, n_runs: int = 3) -> dict:
-        """Decode tokens/s after the prompt (timed like generate_torch.py:
-        280-320, but with the step graph replayed back to back)."""
-        n_prompt = len(prompt_tokens)
-        self.reset(prompt_tokens)
-        self.capture()
-        times = []
-        for _ in range(n_runs):
-            self.reset(prompt_tokens)
-            self.capture()
-            self.run(n_prompt)          # prompt (teacher forced) + first token chosen
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            self.run(n_generate - 1)    # the rest of the continuation
-            torch.cuda.synchronize()
-            times.append(time.perf_counter() - t0)
-        t = sorted(times)[len(times) // 2]
-        return {"generate_tps": (n_generate - 1) / t, "per_token_ms": t / (n_generate - 1) * 1e3,
-                "runs": len(times)}
+        toks = super().generate(prompt_tokens, n_generate)
+        if self.error():
+            raise _lib.NativeBitError(_lib.NB_ELAUNCH, "nb_decode_persistent: a grid barrier "
+                                      "wait ran past its spin limit")
+        return toks

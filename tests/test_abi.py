@@ -242,3 +242,67 @@ def test_silu_mul_validation():
     assert lib.nb_silu_mul(FAKE, FAKE, _lib.NB_BF16, 0, None) == _lib.NB_EINVAL
     assert lib.nb_silu_mul(None, FAKE, _lib.NB_BF16, 8, None) == _lib.NB_EINVAL
     assert lib.nb_silu_mul(FAKE, FAKE, 3, 8, None) == _lib.NB_EINVAL
+
+
+def decode_model(**kw):
+    a = dict(n_layers=26, n_embd=2560, n_head=20, head_dim=128, ffn_hidden=6912, vocab=32000,
+             ctx=1024, eps=1e-6, layers=FAKE, ln_f=FAKE, emb_f32=FAKE, emb_bf16=FAKE,
+             rope_cos=FAKE, rope_sin=FAKE)
+    a.update(kw)
+    return _lib.DecodeModel(*a.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(n_layers=0), _lib.NB_EINVAL),
+    (dict(n_layers=65), _lib.NB_EUNSUPPORTED),
+    (dict(n_embd=2500, n_head=20, head_dim=125), _lib.NB_EUNSUPPORTED),
+    (dict(n_embd=8192, n_head=64), _lib.NB_EUNSUPPORTED),
+    (dict(ffn_hidden=8320), _lib.NB_EUNSUPPORTED),
+    (dict(head_dim=64), _lib.NB_EUNSUPPORTED),           # n_head * head_dim != n_embd
+    (dict(n_head=10, head_dim=256), _lib.NB_EUNSUPPORTED),
+    (dict(ctx=1025), _lib.NB_EUNSUPPORTED),
+    (dict(eps=-1.0), _lib.NB_EINVAL),
+    (dict(layers=None), _lib.NB_EINVAL),
+    (dict(emb_bf16=FAKE + 8), _lib.NB_EALIGN),
+])
+def test_decode_model_validation(kw, status):
+    lib = _lib.load()
+    m = decode_model(**kw)
+    assert lib.nb_decode_workspace_bytes(ctypes.byref(m)) == 0
+    st = lib.nb_decode_persistent(ctypes.byref(m), FAKE, 1 << 30, FAKE, None, None, 0, None, 0,
+                                  4, 0, None)
+    assert st == status, _lib.last_error()
+
+
+def test_decode_persistent_validation():
+    lib = _lib.load()
+    m = decode_model()
+    need = lib.nb_decode_workspace_bytes(ctypes.byref(m))
+    # control block + residual, q|k|v, attention output, gate|up, attention partials
+    assert need >= 4096 + 2560 * 4 + 3 * 2560 * 4 + 2560 * 2 + 2 * 6912 * 4
+    assert need % 256 == 0
+
+    def call(**kw):
+        a = dict(model=ctypes.byref(m), ws=FAKE, ws_bytes=need, state=FAKE, logits=None,
+                 tokens=None, tokens_cap=0, force=None, n_force=0, n_steps=4, spin_limit=0,
+                 stream=None)
+        a.update(kw)
+        return lib.nb_decode_persistent(*a.values())
+
+    assert call(ws_bytes=need - 1) == _lib.NB_EINVAL
+    assert call(ws=None) == _lib.NB_EINVAL
+    assert call(state=None) == _lib.NB_EINVAL
+    assert call(n_steps=-1) == _lib.NB_EINVAL
+    assert call(n_force=2) == _lib.NB_EINVAL
+    assert call(tokens_cap=3) == _lib.NB_EINVAL
+    assert call(ws=FAKE + 128) == _lib.NB_EALIGN
+    assert call(model=None) == _lib.NB_EINVAL
+    assert call(n_steps=0) == _lib.NB_OK          # nothing to do, nothing launched
+    if not gpu_available():
+        assert call() == _lib.NB_ENODEV
+
+
+def test_decode_struct_layout():
+    # the ctypes mirrors of struct nb_decode_layer / nb_decode_model
+    assert ctypes.sizeof(_lib.DecodeLayer) == 12 * 8
+    assert _lib.DecodeModel.layers.offset == 32 and ctypes.sizeof(_lib.DecodeModel) == 32 + 6 * 8
