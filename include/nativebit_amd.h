@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define NB_ABI_VERSION 1
+#define NB_ABI_VERSION 2
 
 enum nb_status {
     NB_OK = 0,
@@ -156,14 +156,38 @@ int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out,
  * memory once and passes it to nb_gemv_batched() (with the same items) on
  * every call.  x, packed and codebook of every item must be 16-byte aligned
  * and K % 128 == 0, K <= 8192.
+ *
+ * Fused activation and output forms (for the layers of a decode step, so
+ * that the norm, the SwiGLU product and the residual add need no launches
+ * of their own).  x_mode says how the item's K bf16 activations a[k] are
+ * formed from x; every workgroup forms them itself, in fp32, rounded to
+ * bf16 (nearest even) once:
+ *   NB_X_BF16      a = x, K bf16 values (the plain batched GEMV);
+ *   NB_X_RMSNORM   x is K fp32 values, a[k] = (x[k] / sqrt(mean(x^2) + eps))
+ *                  * norm_w[k]  (RMSNorm.forward, inference/generate_torch.py:
+ *                  29-38, whose output feeds q|k|v and gate|up, 126-131);
+ *   NB_X_SILU_MUL  x is 2K fp32 values gate | up, a[k] = silu(x[k]) * x[K+k]
+ *                  (SwiGLU, inference/generate_torch.py:116-117).
+ * y_mode: NB_Y_STORE writes y = result; NB_Y_ADD updates y[n] += result in
+ * fp32 (y_dtype NB_F32 only; the residual adds of TransformerBlock.forward,
+ * inference/generate_torch.py:128-132).  The y of an NB_Y_ADD item must not
+ * overlap any x or norm_w of the same batch.  Zero-filled new fields select
+ * the plain GEMV.
  */
+enum nb_x_mode { NB_X_BF16 = 0, NB_X_RMSNORM = 1, NB_X_SILU_MUL = 2 };
+enum nb_y_mode { NB_Y_STORE = 0, NB_Y_ADD = 1 };
 typedef struct nb_batch_item {
-    const void* x;          /* K bf16 activations                          */
+    const void* x;          /* activations, see x_mode                     */
     const uint8_t* packed;  /* 3-bit stream of N*K indices                 */
     const float* codebook;  /* (N*K/128) x 8 fp32                          */
     void* y;                /* N outputs of y_dtype                        */
     int32_t N;
     int32_t K;
+    int32_t x_mode;         /* nb_x_mode                                   */
+    int32_t y_mode;         /* nb_y_mode                                   */
+    const float* norm_w;    /* NB_X_RMSNORM: K fp32 weights (else unused)  */
+    float eps;              /* NB_X_RMSNORM: epsilon                       */
+    int32_t reserved;       /* zero                                        */
 } nb_batch_item;
 
 /* Bytes of the device table for `count` items. */

@@ -33,7 +33,14 @@ NB_F32 = 0
 NB_BF16 = 1
 NB_U8 = 2
 
-ABI_VERSION = 1
+# nb_x_mode / nb_y_mode of a batched GEMV item
+NB_X_BF16 = 0
+NB_X_RMSNORM = 1
+NB_X_SILU_MUL = 2
+NB_Y_STORE = 0
+NB_Y_ADD = 1
+
+ABI_VERSION = 2
 
 # Every symbol include/nativebit_amd.h declares: (name, restype, argtypes).
 _P = ctypes.c_void_p
@@ -68,7 +75,10 @@ class BatchItem(ctypes.Structure):
     """struct nb_batch_item (include/nativebit_amd.h)."""
     _fields_ = [("x", ctypes.c_void_p), ("packed", ctypes.c_void_p),
                 ("codebook", ctypes.c_void_p), ("y", ctypes.c_void_p),
-                ("N", ctypes.c_int32), ("K", ctypes.c_int32)]
+                ("N", ctypes.c_int32), ("K", ctypes.c_int32),
+                ("x_mode", ctypes.c_int32), ("y_mode", ctypes.c_int32),
+                ("norm_w", ctypes.c_void_p), ("eps", ctypes.c_float),
+                ("reserved", ctypes.c_int32)]
 
 
 class DecodeState(ctypes.Structure):

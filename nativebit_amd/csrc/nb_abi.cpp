@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <cmath>
 #include <mutex>
 #include <vector>
 
@@ -216,12 +217,16 @@ int nb::build_stream_table(const nb_batch_item* items, int count, StreamProblem*
         if (it.N == 0) continue;
         StreamProblem p;
         memset(&p, 0, sizeof(p));
-        p.x = static_cast<const uint16_t*>(it.x);
+        p.x = it.x;
         p.packed = it.packed;
         p.codebook = it.codebook;
         p.y = it.y;
+        p.norm_w = it.x_mode == NB_X_RMSNORM ? it.norm_w : nullptr;
         p.N = it.N;
         p.K = it.K;
+        p.x_mode = it.x_mode;
+        p.y_mode = it.y_mode;
+        p.eps = it.eps;
         p.bpr = it.K / 128;
         p.nchunks = (int32_t)(((int64_t)it.N * p.bpr + 63) / 64);
         p.chunk_begin = chunk_begin;
@@ -261,6 +266,22 @@ int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* 
             return fail(NB_EALIGN, "%s: item %d x/packed/codebook not 16-byte aligned", fn, i);
         }
         if (!aligned(it.y, 2)) return fail(NB_EALIGN, "%s: item %d y not 2-byte aligned", fn, i);
+        if (it.x_mode < NB_X_BF16 || it.x_mode > NB_X_SILU_MUL) {
+            return fail(NB_EINVAL, "%s: item %d x_mode=%d", fn, i, it.x_mode);
+        }
+        if (it.y_mode != NB_Y_STORE && it.y_mode != NB_Y_ADD) {
+            return fail(NB_EINVAL, "%s: item %d y_mode=%d", fn, i, it.y_mode);
+        }
+        if (it.reserved != 0) return fail(NB_EINVAL, "%s: item %d reserved field not zero", fn, i);
+        if (it.x_mode == NB_X_RMSNORM) {
+            if (!it.norm_w) return fail(NB_EINVAL, "%s: item %d NB_X_RMSNORM without norm_w", fn, i);
+            if (!aligned(it.norm_w, 16)) {
+                return fail(NB_EALIGN, "%s: item %d norm_w not 16-byte aligned", fn, i);
+            }
+            if (!(it.eps >= 0.f) || !std::isfinite(it.eps)) {
+                return fail(NB_EINVAL, "%s: item %d eps=%g", fn, i, (double)it.eps);
+            }
+        }
         chunks += ((int64_t)it.N * (it.K / 128) + 63) / 64;
         if (it.K > mk) mk = it.K;
     }
@@ -310,6 +331,9 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
         ++nprob;
         if (y_dtype == NB_F32 && !aligned(items[i].y, 4)) {
             return fail(NB_EALIGN, "%s: item %d y not 4-byte aligned", fn, i);
+        }
+        if (items[i].y_mode == NB_Y_ADD && y_dtype != NB_F32) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_ADD needs fp32 outputs", fn, i);
         }
     }
     st = ensure_device();

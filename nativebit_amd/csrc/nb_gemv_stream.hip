@@ -118,6 +118,93 @@ struct Meta {
     bool valid;
 };
 
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
+    return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+}
+
+// The K activations of problem s in the form its x_mode names, rounded to
+// bf16 (nearest even) and written in selector order to the column blocks
+// at `col0` (kXColBytes each).  Every thread of the workgroup calls it (an
+// NB_X_RMSNORM problem takes two workgroup barriers for its sum of squares).
+//   NB_X_BF16      a = x                      (K bf16)
+//   NB_X_RMSNORM   a = (x / sqrt(mean(x^2) + eps)) * w   (K fp32; the
+//                  expression of RMSNorm.forward, generate_torch.py:29-38)
+//   NB_X_SILU_MUL  a = silu(gate) * up, gate | up = x   (2K fp32;
+//                  generate_torch.py:116-117)
+__device__ __forceinline__ void stage_problem(const StreamProblem* sp, unsigned char* col0,
+                                              float* red, int tid) {
+    constexpr int NT = 64 * kWaves;
+    const int K = sp->K, bpr = K >> 7, mode = sp->x_mode;
+    float norm = 1.f;
+    if (mode == NB_X_RMSNORM) {
+        const float* xf = static_cast<const float*>(sp->x);
+        float ss = 0.f;
+        for (int e = tid; e < K; e += NT) {
+            const float v = xf[e];
+            ss += v * v;
+        }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float t = 0.f;
+        for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
+        __syncthreads();  // red is free for the next problem
+        norm = sqrtf(t / (float)K + sp->eps);
+    }
+    for (int q = tid; q < bpr * 4; q += NT) {
+        const int c = q >> 2, u = q & 3;
+        const int k0 = c * 128 + u * 32;
+        uint32_t w[16];
+        if (mode == NB_X_BF16) {
+            const u32x4_t* src =
+                reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(sp->x) + k0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const u32x4_t t = *as_global(src + v);
+                w[4 * v] = t.x;
+                w[4 * v + 1] = t.y;
+                w[4 * v + 2] = t.z;
+                w[4 * v + 3] = t.w;
+            }
+        } else {
+            const float* xf = static_cast<const float*>(sp->x);
+            // second operand: the norm weights, or the up half of gate | up
+            const float* bf = mode == NB_X_RMSNORM ? sp->norm_w : xf + K;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                f32x4_t a[4], b[4];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    a[v] = *as_global(reinterpret_cast<const f32x4_t*>(xf + k0 + 16 * h) + v);
+                    b[v] = *as_global(reinterpret_cast<const f32x4_t*>(bf + k0 + 16 * h) + v);
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    float r[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float xv = a[v][e], bv = b[v][e];
+                        if (mode == NB_X_RMSNORM) {
+                            r[e] = (xv / norm) * bv;
+                        } else {
+                            r[e] = (xv / (1.0f + expf(-xv))) * bv;
+                        }
+                    }
+                    w[8 * h + 2 * v] = bf16x2_rne(r[0], r[1]);
+                    w[8 * h + 2 * v + 1] = bf16x2_rne(r[2], r[3]);
+                }
+            }
+        }
+        stage_unit(col0 + c * kXColBytes, u, w);
+    }
+}
+
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4)))
 void gemv_stream_kernel(
     const StreamProblem* __restrict__ probs, StreamRanges ranges, int y_dtype) {
@@ -126,7 +213,7 @@ void gemv_stream_kernel(
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // ---- set-up: the workgroup's chunks, problems, x vectors and counter --
+    // ---- set-up: the workgroup's chunks, problems and counter -------------
     const int g = blockIdx.x;
     const int C0 = ranges.chunk0[g];
     const int C1 = ranges.chunk0[g + 1];
@@ -165,35 +252,12 @@ void gemv_stream_kernel(
     }
     float* ybuf = reinterpret_cast<float*>(xregion + x_bytes);
     int* next_chunk = reinterpret_cast<int*>(ybuf + y_floats);
-    {
-        // x of each problem in selector order: 16-byte unit j = 4u + m of
-        // column block c, at c * kXColBytes + j * 16, holds the activations
-        // of selectors 2m and 2m+1 of unit u (4 bf16 each, in lookup order).
-        int off = 0;
-        for (int i = 0; i < np; ++i) {
-            const StreamProblem& s = probs[p0 + i];
-            for (int q = tid; q < s.bpr * 4; q += 64 * kWaves) {
-                const int c = q >> 2, u = q & 3;
-                const u32x4_t* src = reinterpret_cast<const u32x4_t*>(s.x + c * 128 + u * 32);
-                uint32_t w[16];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const u32x4_t t = *as_global(src + v);
-                    w[4 * v] = t.x;
-                    w[4 * v + 1] = t.y;
-                    w[4 * v + 2] = t.z;
-                    w[4 * v + 3] = t.w;
-                }
-                stage_unit(xregion + off + c * kXColBytes, u, w);
-            }
-            off += s.bpr * kXColBytes;
-        }
-    }
+    float* red = reinterpret_cast<float*>(next_chunk + 4);  // kWaves floats
     for (int e = tid; e < y_floats; e += 64 * kWaves) ybuf[e] = 0.f;
     if (tid == 0) *next_chunk = C0;
     __syncthreads();
 
-    // ---- steady state: waves take chunks from the counter until none is left
+    // ---- ring state: waves take chunks from the counter until none is left
     auto grab = [&]() -> int {
         int t = 0;
         if (lane == 0) t = atomicAdd(next_chunk, 1);
@@ -202,56 +266,84 @@ void gemv_stream_kernel(
     unsigned char* my_ring = ring + wave * kDepth * kSlotBytes;
     const uint32_t my_ring_lds = lds_addr(my_ring);
 
-    const int c_first = grab();
-    if (c_first < C1) {
-        // load cursor (runs kDepth chunks ahead of computation)
-        int li = 0;
-        Prob LP;
-        read_prob(pl, 0, LP);
-        while (c_first >= LP.chunk_end) read_prob(pl, ++li, LP);
-        int lchunk = c_first;
-        bool lvalid = true;
+    // load cursor (runs kDepth chunks ahead of computation)
+    int li = 0;
+    Prob LP = {};
+    int lchunk = 0;
+    bool lvalid = false;
 
-        // Loads the chunk at the load cursor into ring slot `slot`, records
-        // where it belongs and moves the cursor to chunk `next` (taken from
-        // the counter beforehand); past the wave's last chunk it marks the
-        // slot invalid and loads nothing.  In a problem's partial last
-        // chunk, lanes past the end of the stream re-read its last 16 bytes
-        // (their blocks are not live).
-        auto issue = [&](int slot, Meta& m, int next) {
-            m.valid = lvalid;
-            if (!lvalid) return;  // past the wave's last chunk: no load
-            const int lc = lchunk - LP.chunk_begin;
-            const uint32_t dst = __builtin_amdgcn_readfirstlane(my_ring_lds + slot * kSlotBytes);
-            const uint8_t* ip = LP.packed + (int64_t)lc * kChunkIdxBytes + 16 * lane;
-            const uint8_t* cp = reinterpret_cast<const uint8_t*>(LP.codebook) +
-                                (int64_t)lc * kChunkCbBytes + 16 * lane;
-            if ((lc + 1) * kChunkBlocks <= LP.nblocks) {
-                dma16<0>(dst, ip);
-                dma16<1024>(dst, ip);
-                dma16<2048>(dst, ip);
-                dma16<0>(dst + kChunkIdxBytes, cp);
-                dma16<1024>(dst + kChunkIdxBytes, cp);
-            } else {
-                const uint8_t* ilast = LP.packed + (int64_t)LP.nblocks * 48 - 16;
-                const uint8_t* clast =
-                    reinterpret_cast<const uint8_t*>(LP.codebook) + (int64_t)LP.nblocks * 32 - 16;
-                dma16<0>(dst, min(ip, ilast));
-                dma16<0>(dst + 1024, min(ip + 1024, ilast));
-                dma16<0>(dst + 2048, min(ip + 2048, ilast));
-                dma16<0>(dst + kChunkIdxBytes, min(cp, clast));
-                dma16<0>(dst + kChunkIdxBytes + 1024, min(cp + 1024, clast));
-            }
-            m.li = li;
-            m.lc = lc;
-            if (next >= C1) {
-                lvalid = false;  // the wave's last chunk
-            } else {
-                lchunk = next;
-                while (lchunk >= LP.chunk_end) read_prob(pl, ++li, LP);
-            }
-        };
+    // Loads the chunk at the load cursor into ring slot `slot`, records
+    // where it belongs and moves the cursor to chunk `next` (taken from
+    // the counter beforehand); past the wave's last chunk it marks the
+    // slot invalid and loads nothing.  In a problem's partial last
+    // chunk, lanes past the end of the stream re-read its last 16 bytes
+    // (their blocks are not live).
+    auto issue = [&](int slot, Meta& m, int next) {
+        m.valid = lvalid;
+        if (!lvalid) return;  // past the wave's last chunk: no load
+        const int lc = lchunk - LP.chunk_begin;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(my_ring_lds + slot * kSlotBytes);
+        const uint8_t* ip = LP.packed + (int64_t)lc * kChunkIdxBytes + 16 * lane;
+        const uint8_t* cp = reinterpret_cast<const uint8_t*>(LP.codebook) +
+                            (int64_t)lc * kChunkCbBytes + 16 * lane;
+        if ((lc + 1) * kChunkBlocks <= LP.nblocks) {
+            dma16<0>(dst, ip);
+            dma16<1024>(dst, ip);
+            dma16<2048>(dst, ip);
+            dma16<0>(dst + kChunkIdxBytes, cp);
+            dma16<1024>(dst + kChunkIdxBytes, cp);
+        } else {
+            const uint8_t* ilast = LP.packed + (int64_t)LP.nblocks * 48 - 16;
+            const uint8_t* clast =
+                reinterpret_cast<const uint8_t*>(LP.codebook) + (int64_t)LP.nblocks * 32 - 16;
+            dma16<0>(dst, min(ip, ilast));
+            dma16<0>(dst + 1024, min(ip + 1024, ilast));
+            dma16<0>(dst + 2048, min(ip + 2048, ilast));
+            dma16<0>(dst + kChunkIdxBytes, min(cp, clast));
+            dma16<0>(dst + kChunkIdxBytes + 1024, min(cp + 1024, clast));
+        }
+        m.li = li;
+        m.lc = lc;
+        if (next >= C1) {
+            lvalid = false;  // the wave's last chunk
+        } else {
+            lchunk = next;
+            while (lchunk >= LP.chunk_end) read_prob(pl, ++li, LP);
+        }
+    };
 
+    // The first kDepth chunks of each wave are requested before the
+    // activations are formed: the weights do not depend on them, so the
+    // two memory latencies overlap (a small launch pays one, not two).
+    Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
+    {
+        const int c_first = grab();
+        if (c_first < C1) {
+            read_prob(pl, 0, LP);
+            while (c_first >= LP.chunk_end) read_prob(pl, ++li, LP);
+            lchunk = c_first;
+            lvalid = true;
+            issue(0, ma, grab());
+            issue(1, mb, lvalid ? grab() : C1);
+            if constexpr (kDepth == 3) issue(2, mc, lvalid ? grab() : C1);
+        }
+    }
+
+    // ---- activations of the range's problems, staged in LDS ---------------
+    // (16-byte unit j = 4u + m of column block c, at c * kXColBytes + j * 16,
+    // holds the activations of selectors 2m and 2m+1 of unit u)
+    {
+        int off = 0;
+        for (int i = 0; i < np; ++i) {
+            const StreamProblem* sp = probs + p0 + i;
+            stage_problem(sp, xregion + off, red, tid);
+            off += sp->bpr * kXColBytes;
+        }
+    }
+    __syncthreads();
+
+    // ---- steady state -------------------------------------------------------
+    if (ma.valid) {
         int ci = -1;  // problem whose fields are in CP
         Prob CP = {};
 
@@ -326,10 +418,10 @@ void gemv_stream_kernel(
         // for the chunk), read the slot into registers, refill it with the
         // chunk kDepth ahead, and compute -- kDepth chunks are in flight
         // during the arithmetic.  Validity is monotonic: the first invalid
-        // slot ends the wave's work.  The loop issues no other vector-memory
-        // instruction, so the vmcnt waits count ring loads exactly (each
-        // valid slot holds kLoadsPerChunk loads).
-        Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
+        // slot ends the wave's work.  From here on the wave issues no other
+        // vector-memory instruction (the staging loads above have all been
+        // consumed), so the vmcnt waits count ring loads exactly (each valid
+        // slot holds kLoadsPerChunk loads).
         // `after` = valid slots loaded after this one (their loads may stay
         // in flight).
         auto step = [&](int slot, Meta& m, int after) {
@@ -349,9 +441,7 @@ void gemv_stream_kernel(
             issue(slot, m, next);
             compute(r, cur, L, xv);
         };
-        issue(0, ma, grab());
         if constexpr (kDepth == 2) {
-            issue(1, mb, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
                 step(0, ma, mb.valid ? 1 : 0);
@@ -359,8 +449,6 @@ void gemv_stream_kernel(
                 step(1, mb, ma.valid ? 1 : 0);
             }
         } else {
-            issue(1, mb, lvalid ? grab() : C1);
-            issue(2, mc, lvalid ? grab() : C1);
             while (true) {
                 if (!ma.valid) break;
                 step(0, ma, (int)mb.valid + (int)mc.valid);
@@ -370,13 +458,14 @@ void gemv_stream_kernel(
                 step(2, mc, (int)ma.valid + (int)mb.valid);
             }
         }
-        wait_vm<0>();  // (nothing is in flight here; kept as a guard)
     }
+    wait_vm<0>();  // (nothing is in flight here; kept as a guard)
 
     // ---- write the range's outputs (coalesced, after every wave is done) --
     __syncthreads();
     for (int i = 0; i < np; ++i) {
         const ProbL& P = pl[i];
+        const bool add = probs[p0 + i].y_mode == NB_Y_ADD;
         for (int e = tid; e < P.row_b - P.row_a; e += 64 * kWaves) {
             const int row = P.row_a + e;
             float val = ybuf[P.y_off + e];
@@ -386,6 +475,10 @@ void gemv_stream_kernel(
             if (c_last != c_first) val += ybuf[P.carry_off + c_last - P.ca];
             if (y_dtype == NB_BF16) {
                 *as_global_mut(static_cast<bf16_bits*>(P.y) + row) = f32_to_bf16_rne(val);
+            } else if (add) {
+                // residual add: the row belongs to this workgroup alone
+                auto* yp = as_global_mut(static_cast<float*>(P.y) + row);
+                *yp = *yp + val;
             } else {
                 *as_global_mut(static_cast<float*>(P.y) + row) = val;
             }
@@ -412,7 +505,7 @@ static int64_t range_lds(const StreamProblem* hp, int pa, int pb, int a, int b) 
         const int64_t rb = std::min<int64_t>(s.N, ((int64_t)cb * kChunkBlocks + s.bpr - 1) / s.bpr);
         n += (int64_t)s.bpr * kXColBytes + ((rb - ra) + (cb - ca)) * 4;
     }
-    return n + 16;
+    return n + 16 + 64;  // chunk counter, then the norm's partial sums
 }
 
 // Problem holding chunk c (host copy of the table; binary search).

@@ -44,16 +44,20 @@ struct GemvArgs {
 // One GEMV of a batch as the streaming kernel reads it (device table entry,
 // written on the host by nb_gemv_batch_plan).
 struct StreamProblem {
-    const uint16_t* x;        // K bf16 activations
+    const void* x;            // activations in the form x_mode names
     const uint8_t* packed;    // 3-bit stream
     const float* codebook;    // (N*K/128) x 8
     void* y;                  // N outputs
+    const float* norm_w;      // NB_X_RMSNORM weights
     int32_t N, K;
     int32_t bpr;              // 128-weight blocks per row
     int32_t nchunks;          // 64-block chunks: ceil(N * bpr / 64)
     int32_t chunk_begin;      // chunks of all earlier problems
-    int32_t pad[3];
+    int32_t x_mode;           // nb_x_mode
+    int32_t y_mode;           // nb_y_mode
+    float eps;                // NB_X_RMSNORM epsilon
 };
+static_assert(sizeof(StreamProblem) == 72, "StreamProblem layout");
 
 // Chunk ranges of one streaming launch (kernel argument, by value):
 // workgroup g owns chunks [chunk0[g], chunk0[g+1]) of problems prob0[g] ..

@@ -6,9 +6,11 @@ device memory, so no token needs a host round trip (the reference
 synchronises on ``int(logits.argmax())`` every token, generate_torch.py:311).
 
 * ``DecodeEngine``: a token is a fixed sequence of gfx950 launches -- per
-  layer nb_add_rmsnorm -> q|k|v GEMV -> nb_attention_step -> o GEMV ->
-  nb_add_rmsnorm -> gate|up GEMV -> nb_silu_mul -> down GEMV, then the final
-  norm and nb_lm_head_argmax -- captured once in a HIP graph and replayed.
+  layer q|k|v GEMV (RMSNorm formed in its prologue) -> nb_attention_step ->
+  o GEMV (residual add in its epilogue) -> gate|up GEMV (RMSNorm prologue)
+  -> down GEMV (silu(gate) * up prologue, residual add epilogue), after the
+  embedding lookup and before the final norm and nb_lm_head_argmax --
+  captured once in a HIP graph and replayed.
 * ``PersistentDecodeEngine``: nb_decode_persistent runs many tokens in one
   cooperative launch, the phases of a token separated by grid barriers and
   the packed weights of the next phases streamed during each barrier.
@@ -168,23 +170,30 @@ class DecodeEngine(_DecoderBase):
         super().__init__(model, max_steps)
         C, F, H = self.C, self.F, self.H
         z, bf16 = self._z, torch.bfloat16
-        self.x = z(C)
-        self.h = z(C, dt=bf16)
+        self.x = z(C)                # residual stream (fp32)
+        self.h = z(C, dt=bf16)       # normalised embedding row (layer 0) and final norm
         self.qkv = z(3 * C)
         self.att = z(C, dt=bf16)
-        self.o = z(C)
         self.gu = z(2 * F)
-        self.act = z(F, dt=bf16)
-        self.d = z(C)
         self.work = z(int(_lib.load().nb_attention_work_floats(H)))
         self.done = z(H, dt=torch.int32)
+        # Fused forms of the packed GEMVs (nb_batch_item x_mode / y_mode):
+        # the norms, silu(gate) * up and the residual adds of the reference's
+        # block (generate_torch.py:126-132) happen inside the GEMV launches.
+        # Layer 0's q|k|v reads h, the normalised embedding row.
+        eps = self.eps
+        add = {"y": "add"}
         self.gemvs = []
-        for (qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c) in self.fused:
+        for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
+            ln1, ln2 = self.norms[l]
+            qkv_item = ((self.h, qkv_p, qkv_c, self.qkv, 3 * C, C) if l == 0 else
+                        (self.x, qkv_p, qkv_c, self.qkv, 3 * C, C, {"x": ("rmsnorm", ln1, eps)}))
             self.gemvs.append((
-                ops.GemvBatch([(self.h, qkv_p, qkv_c, self.qkv, 3 * C, C)]),
-                ops.GemvBatch([(self.att, o_p, o_c, self.o, C, C)]),
-                ops.GemvBatch([(self.h, gu_p, gu_c, self.gu, 2 * F, C)]),
-                ops.GemvBatch([(self.act, d_p, d_c, self.d, C, F)]),
+                ops.GemvBatch([qkv_item]),
+                ops.GemvBatch([(self.att, o_p, o_c, self.x, C, C, add)]),
+                ops.GemvBatch([(self.x, gu_p, gu_c, self.gu, 2 * F, C,
+                                {"x": ("rmsnorm", ln2, eps)})]),
+                ops.GemvBatch([(self.gu, d_p, d_c, self.x, C, F, {"x": "silu_mul", "y": "add"})]),
             ))
         self.graph = None
 
@@ -198,28 +207,21 @@ class DecodeEngine(_DecoderBase):
         s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
         ck = _lib.check
         st = _ptr(self.state_t)
-        C, F = self.C, self.F
+        C = self.C
         BF = _lib.NB_BF16
+        # x = embedding[token], h = rmsnorm(x) * ln1 of layer 0
+        ck(lib.nb_add_rmsnorm(_ptr(self.x), None, _ptr(self.emb_f32), st, _ptr(self.norms[0][0]),
+                              _ptr(self.h), BF, C, self.eps, s))
         for l, (g_qkv, g_o, g_gu, g_d) in enumerate(self.gemvs):
-            ln1, ln2 = self.norms[l]
-            if l == 0:
-                ck(lib.nb_add_rmsnorm(_ptr(self.x), None, _ptr(self.emb_f32), st, _ptr(ln1),
-                                      _ptr(self.h), BF, C, self.eps, s))
-            else:
-                ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.d), None, st, _ptr(ln1),
-                                      _ptr(self.h), BF, C, self.eps, s))
-            g_qkv.run()
+            g_qkv.run()                      # qkv = W_qkv rmsnorm(x)
             ck(lib.nb_attention_step(_ptr(self.qkv), _ptr(self.kc[l]), _ptr(self.vc[l]),
                                      _ptr(self.cos), _ptr(self.sin), st, _ptr(self.work),
                                      _ptr(self.done), _ptr(self.att), BF, self.H, self.D,
                                      self.ctx, s))
-            g_o.run()
-            ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.o), None, st, _ptr(ln2), _ptr(self.h),
-                                  BF, C, self.eps, s))
-            g_gu.run()
-            ck(lib.nb_silu_mul(_ptr(self.gu), _ptr(self.act), BF, F, s))
-            g_d.run()
-        ck(lib.nb_add_rmsnorm(_ptr(self.x), _ptr(self.d), None, st, _ptr(self.ln_f), _ptr(self.h),
+            g_o.run()                        # x += W_o att
+            g_gu.run()                       # gu = W_gu rmsnorm(x)
+            g_d.run()                        # x += W_down (silu(gate) * up)
+        ck(lib.nb_add_rmsnorm(_ptr(self.x), None, None, st, _ptr(self.ln_f), _ptr(self.h),
                               BF, C, self.eps, s))
         ck(lib.nb_lm_head_argmax(_ptr(self.h), _ptr(self.emb_bf16), _ptr(self.logits), st,
                                  _ptr(self.tokens), self.max_steps, _ptr(self.force), self.n_force,

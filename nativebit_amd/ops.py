@@ -91,25 +91,62 @@ def gemv(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
 
 
 class GemvBatch:
-    """Many independent 3-bit GEMVs (bf16 x, M = 1) in one persistent launch.
+    """Many independent 3-bit GEMVs (M = 1) in one persistent launch.
 
-    items: sequence of (x, packed, codebook, y, N, K) with x a (K,) bf16
-    tensor, packed/codebook a 3-bit / 8-entry / block-128 layer and y an (N,)
-    float32 or bfloat16 output.  The device table is built once here; each
-    run() enqueues one launch on torch's current stream (graph-capturable).
-    The tensors are referenced by pointer: keep them alive and in place.
+    items: sequence of (x, packed, codebook, y, N, K) or (x, packed,
+    codebook, y, N, K, form), packed/codebook a 3-bit / 8-entry / block-128
+    layer and y an (N,) float32 or bfloat16 output.  ``form`` (a dict, all
+    keys optional) selects the fused activation and output forms of
+    nb_batch_item:
+
+    * ``x``: "bf16" (default; x is (K,) bfloat16), ("rmsnorm", w, eps) (x is
+      the (K,) float32 residual stream, the activations are
+      bf16((x / sqrt(mean(x^2) + eps)) * w), generate_torch.py:29-38) or
+      "silu_mul" (x is the (2K,) float32 gate | up vector, the activations
+      are bf16(silu(gate) * up), generate_torch.py:116-117);
+    * ``y``: "store" (default) or "add" (y += result, float32 y; the
+      residual add, generate_torch.py:128-132).
+
+    The device table is built once here; each run() enqueues one launch on
+    torch's current stream (graph-capturable).  The tensors are referenced
+    by pointer: keep them alive and in place.
     """
 
     def __init__(self, items):
         self.items = list(items)
         n = len(self.items)
         self._arr = (_lib.BatchItem * max(n, 1))()
+        self._keep = []
         y_dt = None
-        for i, (x, packed, cb, y, N, K) in enumerate(self.items):
+        for i, item in enumerate(self.items):
+            x, packed, cb, y, N, K = item[:6]
+            form = item[6] if len(item) > 6 else {}
             for name, t in (("x", x), ("packed", packed), ("codebook", cb), ("y", y)):
                 _require_cuda(name, t)
-            if x.dtype != torch.bfloat16 or x.numel() != K or not x.is_contiguous():
-                raise TypeError(f"item {i}: x must be a contiguous ({K},) bfloat16 tensor")
+            xf = form.get("x", "bf16")
+            norm_w, eps = None, 0.0
+            if xf == "bf16":
+                x_mode, x_dt, x_n = _lib.NB_X_BF16, torch.bfloat16, K
+            elif xf == "silu_mul":
+                x_mode, x_dt, x_n = _lib.NB_X_SILU_MUL, torch.float32, 2 * K
+            elif isinstance(xf, tuple) and xf[0] == "rmsnorm":
+                x_mode, x_dt, x_n = _lib.NB_X_RMSNORM, torch.float32, K
+                norm_w, eps = xf[1], float(xf[2])
+                _require_cuda("norm weight", norm_w)
+                if norm_w.dtype != torch.float32 or norm_w.numel() != K or \
+                        not norm_w.is_contiguous():
+                    raise TypeError(f"item {i}: norm weight must be a contiguous ({K},) float32 tensor")
+                self._keep.append(norm_w)
+            else:
+                raise ValueError(f"item {i}: unknown activation form {xf!r}")
+            if x.dtype != x_dt or x.numel() != x_n or not x.is_contiguous():
+                raise TypeError(f"item {i}: x must be a contiguous ({x_n},) {x_dt} tensor")
+            yf = form.get("y", "store")
+            if yf not in ("store", "add"):
+                raise ValueError(f"item {i}: unknown output form {yf!r}")
+            y_mode = _lib.NB_Y_ADD if yf == "add" else _lib.NB_Y_STORE
+            if yf == "add" and y.dtype != torch.float32:
+                raise TypeError(f"item {i}: y += result needs a float32 y")
             if packed.dtype != torch.uint8 or cb.dtype != torch.float32:
                 raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
             if cb.shape != (N * K // 128, 8) or packed.numel() < packed_nbytes(N * K, 3):
@@ -121,7 +158,9 @@ class GemvBatch:
             elif y.dtype != y_dt:
                 raise TypeError("all outputs of a batch share one dtype")
             self._arr[i] = _lib.BatchItem(x.data_ptr(), packed.data_ptr(), cb.data_ptr(),
-                                          y.data_ptr(), int(N), int(K))
+                                          y.data_ptr(), int(N), int(K), x_mode, y_mode,
+                                          norm_w.data_ptr() if norm_w is not None else None,
+                                          eps, 0)
         self.y_dtype = y_dt or torch.float32
         lib = _lib.load()
         nbytes = int(lib.nb_gemv_batch_table_bytes(n))

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
     assert declared() <= exported
     for name in declared():
         assert getattr(lib, name) is not None
-    assert lib.nb_abi_version() == 1
+    assert lib.nb_abi_version() == 2
 
 
 def test_packed_nbytes(golden):
@@ -157,6 +157,37 @@ def test_batch_validation():
     assert lib.nb_gemv_batched(arr, FAKE, 2, 7, None) == _lib.NB_EINVAL
     empty = (Item * 1)(Item(None, None, None, None, 0, 256))
     assert lib.nb_gemv_batched(empty, None, 1, _lib.NB_F32, None) == _lib.NB_OK
+
+
+def test_batch_fused_forms_validation():
+    """x_mode / y_mode / norm_w / eps of nb_batch_item, checked on the host."""
+    lib = _lib.load()
+    Item = _lib.BatchItem
+    nbytes = lib.nb_gemv_batch_table_bytes(1)
+    buf = ctypes.create_string_buffer(nbytes)
+    X, Y = _lib.NB_X_RMSNORM, _lib.NB_Y_ADD
+
+    def plan(*a):
+        one = (Item * 1)(Item(*a))
+        return lib.nb_gemv_batch_plan(one, 1, buf, nbytes)
+
+    def batched(y_dtype, *a):
+        one = (Item * 1)(Item(*a))
+        return lib.nb_gemv_batched(one, FAKE, 1, y_dtype, None)
+
+    base = (FAKE, FAKE, FAKE, FAKE, 32, 256)
+    assert plan(*base, X, Y, FAKE, 1e-5, 0) == _lib.NB_OK
+    assert plan(*base, _lib.NB_X_SILU_MUL, 0, None, 0.0, 0) == _lib.NB_OK
+    assert plan(*base, 3, 0, None, 0.0, 0) == _lib.NB_EINVAL           # unknown x_mode
+    assert plan(*base, -1, 0, None, 0.0, 0) == _lib.NB_EINVAL
+    assert plan(*base, 0, 2, None, 0.0, 0) == _lib.NB_EINVAL           # unknown y_mode
+    assert plan(*base, X, 0, None, 1e-5, 0) == _lib.NB_EINVAL          # rmsnorm without weights
+    assert plan(*base, X, 0, FAKE + 4, 1e-5, 0) == _lib.NB_EALIGN      # weights misaligned
+    assert plan(*base, X, 0, FAKE, -1.0, 0) == _lib.NB_EINVAL          # negative eps
+    assert plan(*base, X, 0, FAKE, float("nan"), 0) == _lib.NB_EINVAL
+    assert plan(*base, 0, 0, None, 0.0, 1) == _lib.NB_EINVAL           # reserved not zero
+    # y += result is fp32 only
+    assert batched(_lib.NB_BF16, *base, 0, Y, None, 0.0, 0) == _lib.NB_EUNSUPPORTED
 
 
 # --- prefill and decode-step entry points: host-side validation -------------

@@ -397,6 +397,83 @@ def test_batched_full_model_layer(dev):
         assert rel(y.cpu(), ref) <= REL_F32
 
 
+def _fused_activations(mode, x, w=None, eps=0.0):
+    """bf16 activations of an x_mode, formed on the CPU in fp32 by the
+    reference's expressions (RMSNorm: generate_torch.py:35-38; SwiGLU:
+    116-117)."""
+    x = x.detach().cpu().float()
+    if mode == "rmsnorm":
+        norm = torch.sqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+        a = x / norm * w.detach().cpu().float()
+    else:
+        K = x.numel() // 2
+        a = torch.nn.functional.silu(x[:K]) * x[K:]
+    return a.to(torch.bfloat16)
+
+
+def test_batched_fused_forms(dev):
+    """x_mode RMSNorm / SiLU*up and y_mode add in one launch, ragged N: each
+    item equals the unfused sequence (activations formed by torch on the CPU,
+    plain batched GEMV, residual add by torch) and the fp64 brute force over
+    those activations.  Rounding the activations to bf16 may flip a few
+    last bits where the sum of squares is accumulated in another order, so
+    the fused-vs-unfused bar is rel 1e-3, not equality."""
+    g = torch.Generator().manual_seed(77)
+    eps = 1e-6
+    cases = [("rmsnorm", 2560, 2560, "store"), ("silu_mul", 2560, 6912, "add"),
+             ("rmsnorm", 6912, 2560, "add"), ("silu_mul", 100, 256, "store"),
+             ("bf16", 1000, 2560, "add")]
+    items, plain, refs, adds = [], [], [], []
+    for i, (mode, N, K, yf) in enumerate(cases):
+        note(f"fused item {i} {mode} {N}x{K} y={yf}")
+        idx, p, cb = random_layer(N, K, 3, 8, 128, 1300 + i)
+        pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+        form = {"y": yf}
+        if mode == "rmsnorm":
+            x = torch.randn(K, generator=g) * 3
+            w = 1 + 0.1 * torch.randn(K, generator=g)
+            form["x"] = ("rmsnorm", w.to(dev), eps)
+            a = _fused_activations(mode, x, w, eps)
+        elif mode == "silu_mul":
+            x = torch.randn(2 * K, generator=g) * 2
+            form["x"] = "silu_mul"
+            a = _fused_activations(mode, x)
+        else:
+            x = torch.randn(K, generator=g).to(torch.bfloat16)
+            a = x
+        y0 = torch.randn(N, generator=g) if yf == "add" else torch.zeros(N)
+        y = y0.clone().to(dev) if yf == "add" else torch.full((N,), float("nan"), device=dev)
+        items.append((x.to(dev), pt, ct, y, N, K, form))
+        yp = torch.empty(N, device=dev)
+        plain.append((a.to(dev), pt, ct, yp, N, K))
+        refs.append(ref_gemv(a, idx, cb, 128, N, K)[0] + y0.double().numpy())
+        adds.append(y0)
+    ops.GemvBatch(items).run()
+    ops.GemvBatch(plain).run()
+    for i, (item, pl) in enumerate(zip(items, plain)):
+        y, yp = item[3], pl[3]
+        unfused = yp.cpu() + adds[i]
+        assert rel(y.cpu(), unfused) <= 1e-3, (i, rel(y.cpu(), unfused))
+        assert rel(y.cpu(), refs[i]) <= REL_F32, (i, rel(y.cpu(), refs[i]))
+
+
+def test_batched_add_twice_accumulates(dev):
+    """y_mode add reads y each launch: two runs add the product twice."""
+    N, K = 2560, 2560
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 4343)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    x = torch.randn(K, device=dev).to(torch.bfloat16)
+    y0 = torch.randn(N, device=dev)
+    y = y0.clone()
+    b = ops.GemvBatch([(x, pt, ct, y, N, K, {"y": "add"})])
+    b.run()
+    once = y.clone()
+    b.run()
+    yp = ops.gemv(x, pt, ct, N, K)
+    assert rel((once - y0).cpu(), yp.cpu()) <= 1e-5
+    assert rel((y - y0).cpu(), (2 * yp).cpu()) <= 1e-5
+
+
 def test_batched_graph_replay(dev):
     """Captured in a HIP graph and replayed several times, with eager work in
     between, every replay reproduces the eager result."""
