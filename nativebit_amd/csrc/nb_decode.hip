@@ -262,14 +262,16 @@ __global__ void silu_mul_kernel(const float* __restrict__ gu, void* __restrict__
 // ---------------------------------------------------------------------------
 // tied LM head, soft cap, greedy argmax, position advance
 // ---------------------------------------------------------------------------
-// One wave per row at a time: each lane holds 8 * (C / 512) of h's values as
-// fp32 and reads the row's bf16 in 16-byte pieces.  The argmax key is
+// A wave takes kHeadRows rows at a time: lane i reads 16-byte pieces
+// i, i + 64, ... of each row (bf16), with the rows' loads of one piece in
+// flight together, against h staged in LDS as fp32.  The argmax key is
 // (order-preserving bits of the capped logit) << 32 | (0xffffffff - row),
 // so the largest key is the first row with the largest value -- torch's
 // argmax -- whatever the order of the atomics.  The last workgroup to
 // finish (atomic counter) turns the key into the next token.
 constexpr int kHeadThreads = 256;
 constexpr int kHeadMaxC = 8192;
+constexpr int kHeadRows = 8;
 
 __device__ __forceinline__ uint32_t orderable(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -288,26 +290,45 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
     __syncthreads();
     unsigned long long best = 0ull;
     const int nwaves = gridDim.x * (kHeadThreads / 64);
-    for (int r = blockIdx.x * (kHeadThreads / 64) + wave; r < V; r += nwaves) {
-        const bf16_bits* row = emb + (int64_t)r * C;
-        float acc = 0.f;
+    // kHeadRows rows per wave at a time, their loads issued together
+    for (int r0 = (blockIdx.x * (kHeadThreads / 64) + wave) * kHeadRows; r0 < V;
+         r0 += nwaves * kHeadRows) {
+        float acc[kHeadRows];
+#pragma unroll
+        for (int j = 0; j < kHeadRows; ++j) acc[j] = 0.f;
         for (int c = lane * 8; c < C; c += 512) {
             typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
-            const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(row + c));
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            u32x4_t v[kHeadRows];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc += hs[c + 2 * j] * __uint_as_float(wv[j] << 16);
-                acc += hs[c + 2 * j + 1] * __uint_as_float(wv[j] & 0xffff0000u);
+            for (int j = 0; j < kHeadRows; ++j) {
+                const int r = min(r0 + j, V - 1);  // rows past V repeat the last one
+                v[j] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4_t*>(emb + (int64_t)r * C + c));
+            }
+            float hv[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) hv[e] = hs[c + e];
+#pragma unroll
+            for (int j = 0; j < kHeadRows; ++j) {
+                const uint32_t wv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[j] += hv[2 * e] * __uint_as_float(wv[e] << 16);
+                    acc[j] += hv[2 * e + 1] * __uint_as_float(wv[e] & 0xffff0000u);
+                }
             }
         }
-        acc = wave_sum(acc);
-        const float capped = 30.0f * tanhf(acc / 30.0f);
-        if (lane == 0) {
-            if (logits) logits[r] = capped;
-            const unsigned long long key =
-                ((unsigned long long)orderable(capped) << 32) | (0xffffffffu - (uint32_t)r);
-            best = key > best ? key : best;
+#pragma unroll
+        for (int j = 0; j < kHeadRows; ++j) {
+            const int r = r0 + j;
+            const float sum = wave_sum(acc[j]);
+            const float capped = 30.0f * tanhf(sum / 30.0f);
+            if (lane == 0 && r < V) {
+                if (logits) logits[r] = capped;
+                const unsigned long long key =
+                    ((unsigned long long)orderable(capped) << 32) | (0xffffffffu - (uint32_t)r);
+                best = key > best ? key : best;
+            }
         }
     }
     if (lane == 0) wkey[wave] = best;
@@ -361,7 +382,8 @@ int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t st
 int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* st,
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                           int V, int C, hipStream_t stream) {
-    const int blocks = std::min(1024, (V + 3) / 4);
+    const int rows_per_block = kHeadRows * (kHeadThreads / 64);
+    const int blocks = std::min(1024, (V + rows_per_block - 1) / rows_per_block);
     hipLaunchKernelGGL(lm_head_argmax_kernel, dim3(blocks), dim3(kHeadThreads), 0, stream,
                        static_cast<const bf16_bits*>(h), static_cast<const bf16_bits*>(emb), logits,
                        st, tokens_out, tokens_cap, force, n_force, V, C);

@@ -70,12 +70,15 @@ constexpr int kChunkIdxBytes = kChunkBlocks * 48;  // 3 KiB
 constexpr int kChunkCbBytes = kChunkBlocks * 32;   // 2 KiB
 constexpr int kSlotBytes = kChunkIdxBytes + kChunkCbBytes;
 constexpr int kLoadsPerChunk = 5;
-// One problem of the workgroup's range as the chunk loop reads it, copied
-// into LDS at set-up (64 bytes).
+// One problem of the workgroup's range as the set-up, the activation
+// staging, the chunk loop and the output phase read it, copied into LDS at
+// set-up (96 bytes): after the set-up no phase reads the device table.
 struct ProbL {
     const uint8_t* packed;
     const float* codebook;
     void* y;
+    const void* x;          // activations in the form x_mode names
+    const float* norm_w;    // NB_X_RMSNORM weights
     int32_t nblocks, bpr, nchunks, chunk_begin;
     int32_t x_off;      // byte offset of this problem's x (permuted) in LDS
     int32_t y_off;      // float offset of its row sums (rows row_a..row_b-1)
@@ -83,8 +86,11 @@ struct ProbL {
     int32_t row_b;      // one past the last row
     int32_t carry_off;  // float offset of its carries (chunks ca..)
     int32_t ca;         // first chunk of this problem in the range
+    int32_t x_mode, y_mode;
+    float eps;
+    int32_t pad;
 };
-static_assert(sizeof(ProbL) == 64, "ProbL is 64 bytes");
+static_assert(sizeof(ProbL) == 96, "ProbL is 96 bytes");
 
 // The fields the loop needs, in scalar registers.
 struct Prob {
@@ -124,30 +130,82 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t bf16x2_rne(float lo, float hi) {
-    return (uint32_t)f32_to_bf16_rne(lo) | ((uint32_t)f32_to_bf16_rne(hi) << 16);
+// Halfword position, inside a column block's staged activations, of
+// element e (0..7) of 8-element group g (0..15) of the block: the group's
+// unit u = g / 4 and quarter q = g % 4, element e = index offset o of
+// selector s with sel_offset(s) = e; selector s sits in 16-byte unit
+// 4u + s / 2, halves (s & 1) * 4 + q (stage_unit's layout).
+__device__ __forceinline__ int staged_half(int g, int e) {
+    const int s = e == 0 ? 0 : e == 1 ? 1 : e == 2 ? 6 : e == 3 ? 2 : e == 4 ? 3 : e == 5 ? 7
+                : e == 6 ? 4 : 5;
+    return (4 * (g >> 2) + (s >> 1)) * 8 + (s & 1) * 4 + (g & 3);
 }
 
 // The K activations of problem s in the form its x_mode names, rounded to
 // bf16 (nearest even) and written in selector order to the column blocks
-// at `col0` (kXColBytes each).  Every thread of the workgroup calls it (an
-// NB_X_RMSNORM problem takes two workgroup barriers for its sum of squares).
+// at `col0` (kXColBytes each).  Every thread of the workgroup calls it.
 //   NB_X_BF16      a = x                      (K bf16)
 //   NB_X_RMSNORM   a = (x / sqrt(mean(x^2) + eps)) * w   (K fp32; the
 //                  expression of RMSNorm.forward, generate_torch.py:29-38)
 //   NB_X_SILU_MUL  a = silu(gate) * up, gate | up = x   (2K fp32;
 //                  generate_torch.py:116-117)
-__device__ __forceinline__ void stage_problem(const StreamProblem* sp, unsigned char* col0,
+// The fp32 forms spread 8-element groups over all threads with every load
+// issued up front, so a launch pays one memory round trip for them (plus
+// two workgroup barriers for the norm's sum of squares).  exp(-g) in silu
+// is v_exp_f32 of -g * log2(e) (__expf; a few ulp in fp32, below the bf16
+// rounding that follows).
+__device__ __forceinline__ void stage_problem(const ProbL* sp, unsigned char* col0,
                                               float* red, int tid) {
     constexpr int NT = 64 * kWaves;
-    const int K = sp->K, bpr = K >> 7, mode = sp->x_mode;
+    constexpr int kMaxG = (8192 / 8 + NT - 1) / NT;  // groups per thread (K <= 8192)
+    const int K = sp->bpr * 128, mode = sp->x_mode;
+    if (mode == NB_X_BF16) {
+        for (int q = tid; q < (K >> 5); q += NT) {
+            const int c = q >> 2, u = q & 3;
+            const u32x4_t* src = reinterpret_cast<const u32x4_t*>(
+                static_cast<const uint16_t*>(sp->x) + c * 128 + u * 32);
+            uint32_t w[16];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const u32x4_t t = *as_global(src + v);
+                w[4 * v] = t.x;
+                w[4 * v + 1] = t.y;
+                w[4 * v + 2] = t.z;
+                w[4 * v + 3] = t.w;
+            }
+            stage_unit(col0 + c * kXColBytes, u, w);
+        }
+        return;
+    }
+    const int ng = K >> 3;
+    const float* xf = static_cast<const float*>(sp->x);
+    // second operand: the norm weights, or the up half of gate | up
+    const float* bf = mode == NB_X_RMSNORM ? sp->norm_w : xf + K;
+    f32x4_t a[kMaxG][2], b[kMaxG][2];
+#pragma unroll
+    for (int j = 0; j < kMaxG; ++j) {
+        const int g = tid + j * NT;
+        if (g < ng) {
+            const f32x4_t* xa = reinterpret_cast<const f32x4_t*>(xf + 8 * g);
+            const f32x4_t* xb = reinterpret_cast<const f32x4_t*>(bf + 8 * g);
+            a[j][0] = *as_global(xa);
+            a[j][1] = *as_global(xa + 1);
+            b[j][0] = *as_global(xb);
+            b[j][1] = *as_global(xb + 1);
+        }
+    }
     float norm = 1.f;
     if (mode == NB_X_RMSNORM) {
-        const float* xf = static_cast<const float*>(sp->x);
         float ss = 0.f;
-        for (int e = tid; e < K; e += NT) {
-            const float v = xf[e];
-            ss += v * v;
+#pragma unroll
+        for (int j = 0; j < kMaxG; ++j) {
+            if (tid + j * NT < ng) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ss += a[j][h][e] * a[j][h][e];
+                }
+            }
         }
         ss = wave_sum(ss);
         if ((tid & 63) == 0) red[tid >> 6] = ss;
@@ -157,51 +215,20 @@ __device__ __forceinline__ void stage_problem(const StreamProblem* sp, unsigned 
         __syncthreads();  // red is free for the next problem
         norm = sqrtf(t / (float)K + sp->eps);
     }
-    for (int q = tid; q < bpr * 4; q += NT) {
-        const int c = q >> 2, u = q & 3;
-        const int k0 = c * 128 + u * 32;
-        uint32_t w[16];
-        if (mode == NB_X_BF16) {
-            const u32x4_t* src =
-                reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(sp->x) + k0);
+    uint16_t* out = reinterpret_cast<uint16_t*>(col0);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const u32x4_t t = *as_global(src + v);
-                w[4 * v] = t.x;
-                w[4 * v + 1] = t.y;
-                w[4 * v + 2] = t.z;
-                w[4 * v + 3] = t.w;
-            }
-        } else {
-            const float* xf = static_cast<const float*>(sp->x);
-            // second operand: the norm weights, or the up half of gate | up
-            const float* bf = mode == NB_X_RMSNORM ? sp->norm_w : xf + K;
+    for (int j = 0; j < kMaxG; ++j) {
+        const int g = tid + j * NT;
+        if (g < ng) {
+            uint16_t* col = out + (g >> 4) * (kXColBytes / 2);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                f32x4_t a[4], b[4];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    a[v] = *as_global(reinterpret_cast<const f32x4_t*>(xf + k0 + 16 * h) + v);
-                    b[v] = *as_global(reinterpret_cast<const f32x4_t*>(bf + k0 + 16 * h) + v);
-                }
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    float r[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float xv = a[v][e], bv = b[v][e];
-                        if (mode == NB_X_RMSNORM) {
-                            r[e] = (xv / norm) * bv;
-                        } else {
-                            r[e] = (xv / (1.0f + expf(-xv))) * bv;
-                        }
-                    }
-                    w[8 * h + 2 * v] = bf16x2_rne(r[0], r[1]);
-                    w[8 * h + 2 * v + 1] = bf16x2_rne(r[2], r[3]);
-                }
+            for (int e = 0; e < 8; ++e) {
+                const float xv = a[j][e >> 2][e & 3], bv = b[j][e >> 2][e & 3];
+                const float r = mode == NB_X_RMSNORM ? (xv / norm) * bv
+                                                     : (xv / (1.0f + __expf(-xv))) * bv;
+                col[staged_half(g & 15, e)] = f32_to_bf16_rne(r);
             }
         }
-        stage_unit(col0 + c * kXColBytes, u, w);
     }
 }
 
@@ -245,6 +272,11 @@ void gemv_stream_kernel(
             d.row_b = rb;
             d.carry_off = y_floats + (rb - ra);
             d.ca = ca;
+            d.x = s.x;
+            d.norm_w = s.norm_w;
+            d.x_mode = s.x_mode;
+            d.y_mode = s.y_mode;
+            d.eps = s.eps;
             pl[i] = d;
         }
         x_bytes += s.bpr * kXColBytes;
@@ -316,7 +348,7 @@ void gemv_stream_kernel(
     // activations are formed: the weights do not depend on them, so the
     // two memory latencies overlap (a small launch pays one, not two).
     Meta ma = {0, 0, false}, mb = {0, 0, false}, mc = {0, 0, false};
-    {
+    auto start = [&]() {
         const int c_first = grab();
         if (c_first < C1) {
             read_prob(pl, 0, LP);
@@ -327,18 +359,14 @@ void gemv_stream_kernel(
             issue(1, mb, lvalid ? grab() : C1);
             if constexpr (kDepth == 3) issue(2, mc, lvalid ? grab() : C1);
         }
-    }
+    };
+    start();
 
     // ---- activations of the range's problems, staged in LDS ---------------
     // (16-byte unit j = 4u + m of column block c, at c * kXColBytes + j * 16,
     // holds the activations of selectors 2m and 2m+1 of unit u)
     {
-        int off = 0;
-        for (int i = 0; i < np; ++i) {
-            const StreamProblem* sp = probs + p0 + i;
-            stage_problem(sp, xregion + off, red, tid);
-            off += sp->bpr * kXColBytes;
-        }
+        for (int i = 0; i < np; ++i) stage_problem(pl + i, xregion + pl[i].x_off, red, tid);
     }
     __syncthreads();
 
@@ -465,7 +493,7 @@ void gemv_stream_kernel(
     __syncthreads();
     for (int i = 0; i < np; ++i) {
         const ProbL& P = pl[i];
-        const bool add = probs[p0 + i].y_mode == NB_Y_ADD;
+        const bool add = P.y_mode == NB_Y_ADD;
         for (int e = tid; e < P.row_b - P.row_a; e += 64 * kWaves) {
             const int row = P.row_a + e;
             float val = ybuf[P.y_off + e];
