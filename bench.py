@@ -27,7 +27,9 @@ configurations are reported in the same JSON line under "configs":
   prefill  config 4a: nb_gemm_prefill on one layer's matmuls at M = 512 and
            2048 tokens, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA
            peak, beside torch's dense bf16 matmul of an unpacked weight
-  skinny   config 2: nb_gemv at M = 1, 2, 4, 8, 16 over all 182 matmuls
+  skinny   config 2: M = 1, 2, 4, 8, 16 activation rows over all 182 matmuls,
+           one batched launch per step (nb_gemm_skinny_batched at M > 1),
+           beside 182 per-matmul nb_gemv launches
   sweep    config 3: nb_gemv at batch 1, NE in {4, 8, 16} x BS in {64, 128,
            256} on 6912x2560 and 2560x6912 (random indices and codebooks;
            copies rotated over > 512 MB so no cache holds them)
@@ -326,7 +328,11 @@ def bench_prefill(dev):
 
 
 def bench_skinny(dev, layers):
-    """Config 2: nb_gemv at M rows over all 182 matmuls (graph of launches)."""
+    """Config 2: M activation rows over all 182 matmuls of a step.
+
+    batched: one launch per step -- nb_gemv_batched (the streaming kernel)
+    at M = 1, nb_gemm_skinny_batched at M > 1 -- replayed as a HIP graph;
+    per_matmul: 182 nb_gemv launches per step (one per matmul) in a graph."""
     from nativebit_amd import ops, synth
     mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
     out = {}
@@ -334,17 +340,28 @@ def bench_skinny(dev, layers):
         xs = {K: synth.make_activation(K, m=M, seed=M, device=dev, dtype=torch.bfloat16)
               for K in (2560, 6912)}
         ys = [torch.empty(M, m.N, device=dev) for m in mats]
+        nbytes = sum(synth.layer_bytes(m.N, m.K, NE, BS, M, 2, 4) for m in mats)
+        fl = 2 * M * sum(m.N * m.K for m in mats)
+        batch = ops.GemvBatch([((xs[m.K][0] if M == 1 else xs[m.K]), m.packed, m.cb,
+                                (y[0] if M == 1 else y), m.N, m.K) for m, y in zip(mats, ys)],
+                              m=M)
+        ms_b = graph_time(batch.run, 20, 5)
 
         def run():
             for m, y in zip(mats, ys):
                 ops.gemv(xs[m.K], m.packed, m.cb, m.N, m.K, out=y)
-        ms = graph_time(run, 20, 5)
-        nbytes = sum(synth.layer_bytes(m.N, m.K, NE, BS, M, 2, 4) for m in mats)
-        fl = 2 * M * sum(m.N * m.K for m in mats)
-        out[f"M{M}"] = {"us_per_step": round(ms * 1e3, 1), "GB_s": round(nbytes / ms / 1e6, 1),
-                        "TFLOP_s": round(fl / ms / 1e9, 2)}
-        del ys, xs
-    out["note"] = "182 nb_gemv launches per step (one per matmul), replayed as one HIP graph"
+        ms_p = graph_time(run, 20, 5)
+        out[f"M{M}"] = {"us_per_step": round(ms_b * 1e3, 1), "GB_s": round(nbytes / ms_b / 1e6, 1),
+                        "pct_hbm_peak": round(nbytes / ms_b / 1e6 / HBM_PEAK_GBS * 100, 1),
+                        "TFLOP_s": round(fl / ms_b / 1e9, 2),
+                        "kernel": "gemv_stream_kernel" if M == 1 else "gemv_skinny_kernel",
+                        "per_matmul_us_per_step": round(ms_p * 1e3, 1),
+                        "per_matmul_GB_s": round(nbytes / ms_p / 1e6, 1)}
+        log(f"[bench] skinny M={M}: batched {ms_b*1e3:.1f} us ({nbytes/ms_b/1e6:.0f} GB/s), "
+            f"per-matmul launches {ms_p*1e3:.1f} us")
+        del ys, xs, batch
+    out["note"] = ("batched: every matmul of the step in one launch (graph replay); "
+                   "per_matmul: 182 nb_gemv launches per step in one graph")
     return out
 
 

@@ -203,6 +203,17 @@ int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
 int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count,
                     int y_dtype, void* stream);
 
+/* Batched skinny GEMM: the same batch with M (1..16) activation rows per
+ * item -- the batched branch of PackedLinear.forward (inference/
+ * triton_kernel.py:258-275) in its bf16 form (inference/eval_ppl.py:149-174)
+ * for every packed layer of a small-batch decode step, in one launch:
+ *   y[m][n] = sum_k x[m][k] * bf16(W[n][k])   (fp32 accumulation)
+ * with x an M x K bf16 row-major matrix (row stride K) and y M x N
+ * row-major (row stride N) of y_dtype.  Items are x_mode NB_X_BF16 with
+ * y_mode NB_Y_STORE or NB_Y_ADD (fp32); table_dev as for nb_gemv_batched. */
+int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count,
+                           int M, int y_dtype, void* stream);
+
 
 /* ------------------------------------------------------------------------
  * Decode step (one token, batch 1) -- the non-GEMV kernels of the packed

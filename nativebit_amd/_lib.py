@@ -57,6 +57,7 @@ SIGNATURES = {
     "nb_gemv_batch_table_bytes": (_L, [_I]),
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),
+    "nb_gemm_skinny_batched": (_I, [_P, _P, _I, _I, _I, _P]),
     "nb_gemm_prefill": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P]),
     "nb_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P]),
     "nb_attention_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),

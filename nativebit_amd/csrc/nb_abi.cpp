@@ -345,6 +345,40 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
                               y_dtype, static_cast<hipStream_t>(stream));
 }
 
+int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
+                           int y_dtype, void* stream) {
+    const char* fn = "nb_gemm_skinny_batched";
+    int64_t chunks = 0;
+    int mk = 0;
+    int st = check_batch(items, count, fn, &chunks, &mk);
+    if (st) return st;
+    if (M < 1 || M > 16) return fail(NB_EINVAL, "%s: M=%d outside 1..16", fn, M);
+    if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
+    if (chunks == 0) return NB_OK;
+    if (!table_dev) return fail(NB_EINVAL, "%s: table_dev is NULL", fn);
+    if (!aligned(table_dev, 8)) return fail(NB_EALIGN, "%s: table_dev not 8-byte aligned", fn);
+    int nprob = 0;
+    for (int i = 0; i < count; ++i) {
+        if (items[i].N == 0) continue;
+        ++nprob;
+        if (items[i].x_mode != NB_X_BF16) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d: only NB_X_BF16 activations", fn, i);
+        }
+        if (y_dtype == NB_F32 && !aligned(items[i].y, 4)) {
+            return fail(NB_EALIGN, "%s: item %d y not 4-byte aligned", fn, i);
+        }
+        if (items[i].y_mode == NB_Y_ADD && y_dtype != NB_F32) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_ADD needs fp32 outputs", fn, i);
+        }
+    }
+    st = ensure_device();
+    if (st) return st;
+    std::vector<StreamProblem> host((size_t)nprob);
+    build_stream_table(items, count, host.data());
+    return launch_gemv_skinny(static_cast<const StreamProblem*>(table_dev), host.data(), nprob, M,
+                              y_dtype, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"
 
 extern "C" {

@@ -69,6 +69,16 @@ struct StreamRanges {
     int32_t prob1[kStreamMaxGroups];
 };
 
+// Workgroup tasks of one skinny-GEMM launch (kernel argument, by value):
+// problems prob0 .. prob0 + nprob - 1 of the table; problem prob0 + i owns
+// tasks task_begin[i] .. (128 rows each).
+constexpr int kSkinnyMaxProbs = 512;
+struct SkinnyTasks {
+    int32_t task_begin[kSkinnyMaxProbs];
+    int32_t prob0;
+    int32_t nprob;
+};
+
 // Fills `out` (nprob entries) from the batch items with N > 0, in order;
 // returns nprob.
 int build_stream_table(const nb_batch_item* items, int count, StreamProblem* out);
@@ -77,6 +87,11 @@ int build_stream_table(const nb_batch_item* items, int count, StreamProblem* out
 // kernel, host copy to plan the workgroup ranges).
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
                        int nprob, int y_dtype, hipStream_t stream);
+
+// Launches the batched skinny GEMM (M <= 16 activation rows) over the
+// problem table.
+int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host_probs,
+                       int nprob, int M, int y_dtype, hipStream_t stream);
 
 // Kernel launchers (arguments already validated by nb_abi.cpp).
 int launch_gemv(const GemvArgs& a, hipStream_t stream);

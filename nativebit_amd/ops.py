@@ -91,7 +91,7 @@ def gemv(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
 
 
 class GemvBatch:
-    """Many independent 3-bit GEMVs (M = 1) in one persistent launch.
+    """Many independent 3-bit GEMVs in one launch.
 
     items: sequence of (x, packed, codebook, y, N, K) or (x, packed,
     codebook, y, N, K, form), packed/codebook a 3-bit / 8-entry / block-128
@@ -107,12 +107,20 @@ class GemvBatch:
     * ``y``: "store" (default) or "add" (y += result, float32 y; the
       residual add, generate_torch.py:128-132).
 
+    ``m`` > 1 (up to 16) makes every item a skinny GEMM over m activation
+    rows (nb_gemm_skinny_batched): x is an (m, K) bfloat16 matrix and y an
+    (m, N) matrix, both contiguous; only the plain bf16 activation form is
+    available then (the output may still be "add").
+
     The device table is built once here; each run() enqueues one launch on
     torch's current stream (graph-capturable).  The tensors are referenced
     by pointer: keep them alive and in place.
     """
 
-    def __init__(self, items):
+    def __init__(self, items, m: int = 1):
+        if not 1 <= m <= 16:
+            raise ValueError(f"m={m} outside 1..16")
+        self.m = int(m)
         self.items = list(items)
         n = len(self.items)
         self._arr = (_lib.BatchItem * max(n, 1))()
@@ -124,6 +132,8 @@ class GemvBatch:
             for name, t in (("x", x), ("packed", packed), ("codebook", cb), ("y", y)):
                 _require_cuda(name, t)
             xf = form.get("x", "bf16")
+            if m > 1 and xf != "bf16":
+                raise ValueError(f"item {i}: m > 1 takes bf16 activations only")
             norm_w, eps = None, 0.0
             if xf == "bf16":
                 x_mode, x_dt, x_n = _lib.NB_X_BF16, torch.bfloat16, K
@@ -139,8 +149,9 @@ class GemvBatch:
                 self._keep.append(norm_w)
             else:
                 raise ValueError(f"item {i}: unknown activation form {xf!r}")
-            if x.dtype != x_dt or x.numel() != x_n or not x.is_contiguous():
-                raise TypeError(f"item {i}: x must be a contiguous ({x_n},) {x_dt} tensor")
+            if x.dtype != x_dt or x.numel() != m * x_n or not x.is_contiguous():
+                shape = f"({m}, {x_n})" if m > 1 else f"({x_n},)"
+                raise TypeError(f"item {i}: x must be a contiguous {shape} {x_dt} tensor")
             yf = form.get("y", "store")
             if yf not in ("store", "add"):
                 raise ValueError(f"item {i}: unknown output form {yf!r}")
@@ -151,8 +162,9 @@ class GemvBatch:
                 raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
             if cb.shape != (N * K // 128, 8) or packed.numel() < packed_nbytes(N * K, 3):
                 raise ValueError(f"item {i}: not a 3-bit / 8-entry / block-128 {N}x{K} layer")
-            if y.numel() != N or y.dtype not in _DT or not y.is_contiguous():
-                raise ValueError(f"item {i}: y must be a contiguous ({N},) float32/bfloat16 tensor")
+            if y.numel() != m * N or y.dtype not in _DT or not y.is_contiguous():
+                shape = f"({m}, {N})" if m > 1 else f"({N},)"
+                raise ValueError(f"item {i}: y must be a contiguous {shape} float32/bfloat16 tensor")
             if y_dt is None:
                 y_dt = y.dtype
             elif y.dtype != y_dt:
@@ -172,8 +184,13 @@ class GemvBatch:
 
     def run(self):
         stream = ctypes.c_void_p(torch.cuda.current_stream(self.table.device).cuda_stream)
-        _lib.check(_lib.load().nb_gemv_batched(self._arr, self.table.data_ptr(), self.count,
-                                               _DT[self.y_dtype], stream))
+        lib = _lib.load()
+        if self.m == 1:
+            _lib.check(lib.nb_gemv_batched(self._arr, self.table.data_ptr(), self.count,
+                                           _DT[self.y_dtype], stream))
+        else:
+            _lib.check(lib.nb_gemm_skinny_batched(self._arr, self.table.data_ptr(), self.count,
+                                                  self.m, _DT[self.y_dtype], stream))
 
 
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,

@@ -190,6 +190,30 @@ def test_batch_fused_forms_validation():
     assert batched(_lib.NB_BF16, *base, 0, Y, None, 0.0, 0) == _lib.NB_EUNSUPPORTED
 
 
+def test_skinny_batch_validation():
+    """nb_gemm_skinny_batched: M range, bf16 activations only, the shared
+    item checks and the y_dtype / NB_Y_ADD rules, all on the host."""
+    lib = _lib.load()
+    Item = _lib.BatchItem
+    good = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 256))
+    sk = lib.nb_gemm_skinny_batched
+    for M in (0, -1, 17):
+        assert sk(good, FAKE, 1, M, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert sk(good, FAKE, 1, 4, 7, None) == _lib.NB_EINVAL
+    assert sk(good, None, 1, 4, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert sk(good, FAKE + 4, 1, 4, _lib.NB_F32, None) == _lib.NB_EALIGN
+    norm = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 256, _lib.NB_X_RMSNORM, 0, FAKE, 1e-5, 0))
+    assert sk(norm, FAKE, 1, 4, _lib.NB_F32, None) == _lib.NB_EUNSUPPORTED
+    add16 = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 256, 0, _lib.NB_Y_ADD, None, 0.0, 0))
+    assert sk(add16, FAKE, 1, 4, _lib.NB_BF16, None) == _lib.NB_EUNSUPPORTED
+    for bad, st in ((Item(FAKE, FAKE, FAKE, FAKE, 32, 200), _lib.NB_EUNSUPPORTED),
+                    (Item(FAKE + 8, FAKE, FAKE, FAKE, 32, 256), _lib.NB_EALIGN),
+                    (Item(FAKE, FAKE, FAKE, FAKE, -1, 256), _lib.NB_EINVAL)):
+        assert sk((Item * 1)(bad), FAKE, 1, 4, _lib.NB_F32, None) == st
+    empty = (Item * 1)(Item(None, None, None, None, 0, 256))
+    assert sk(empty, None, 1, 4, _lib.NB_F32, None) == _lib.NB_OK
+
+
 # --- prefill and decode-step entry points: host-side validation -------------
 
 def prefill(**kw):

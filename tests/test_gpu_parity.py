@@ -7,11 +7,13 @@ Bars (from the north star):
   bf16, inference/eval_ppl.py:149-174) for bf16 activations; golden cases
   with fp32-exact answers must match exactly.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
-from nativebit_amd import PackedLinear, kernels, ops, synth
+from nativebit_amd import PackedLinear, _lib, kernels, ops, synth
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -472,6 +474,60 @@ def test_batched_add_twice_accumulates(dev):
     yp = ops.gemv(x, pt, ct, N, K)
     assert rel((once - y0).cpu(), yp.cpu()) <= 1e-5
     assert rel((y - y0).cpu(), (2 * yp).cpu()) <= 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
+def test_skinny_batched_vs_f64(dev, M):
+    """nb_gemm_skinny_batched over mixed shapes (ragged N, K with a partial
+    last 512-slice, an empty item) equals the fp64 brute force on the
+    bf16-rounded weights for every activation row."""
+    shapes = [(2560, 2560), (100, 384), (0, 2560), (1000, 6912), (17, 128), (300, 2688)]
+    items, refs = [], []
+    for i, (N, K) in enumerate(shapes):
+        note(f"skinny M={M} item {i} {N}x{K}")
+        idx, p, cb = random_layer(max(N, 1), K, 3, 8, 128, 1500 + 10 * M + i)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(i + M)).to(torch.bfloat16)
+        pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+        if N == 0:
+            pt, ct = pt[:16].clone(), ct[:0].reshape(0, 8).contiguous()
+        y = torch.full((M, N), float("nan"), device=dev)
+        items.append((x.to(dev).contiguous(), pt, ct, y, N, K))
+        refs.append(ref_gemv(x, idx, cb, 128, N, K) if N else None)
+    b = ops.GemvBatch(items, m=M)
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    # the skinny kernel itself, also at M = 1 (GemvBatch(m=1) streams)
+    _lib.check(lib.nb_gemm_skinny_batched(b._arr, b.table.data_ptr(), b.count, M, _lib.NB_F32,
+                                          stream))
+    torch.cuda.synchronize()
+    for i, (x, pt, ct, y, N, K) in enumerate(items):
+        if N:
+            assert rel(y.cpu(), refs[i]) <= REL_F32, (i, rel(y.cpu(), refs[i]))
+    if M > 1:
+        y1 = [t[3].clone() for t in items]
+        b.run()
+        for (x, pt, ct, y, N, K), ya in zip(items, y1):
+            assert torch.equal(y, ya)  # deterministic
+
+
+def test_skinny_batched_forms(dev):
+    """bf16 outputs are the rounded fp32 outputs; y_mode add adds."""
+    M, N, K = 4, 2560, 6912
+    idx, p, cb = random_layer(N, K, 3, 8, 128, 1777)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    x = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    y32 = torch.empty(M, N, device=dev)
+    ops.GemvBatch([(x, pt, ct, y32, N, K)], m=M).run()
+    y16 = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    ops.GemvBatch([(x, pt, ct, y16, N, K)], m=M).run()
+    assert torch.equal(y16, y32.to(torch.bfloat16))
+    y0 = torch.randn(M, N, device=dev)
+    ya = y0.clone()
+    ops.GemvBatch([(x, pt, ct, ya, N, K, {"y": "add"})], m=M).run()
+    assert rel((ya - y0).cpu(), y32.cpu()) <= 1e-5
+    # row m of a skinny product is the M = 1 GEMV of x[m]
+    for m in range(M):
+        assert rel(y32[m].cpu(), ops.gemv(x[m].contiguous(), pt, ct, N, K).cpu()) <= 1e-5
 
 
 def test_batched_graph_replay(dev):
