@@ -79,6 +79,10 @@ def parse():
                    help="skip the decode / prefill / skinny / sweep configurations")
     p.add_argument("--extra", default="decode,prefill,skinny,sweep",
                    help="comma list of extra configurations to run")
+    p.add_argument("--random-weights", action="store_true",
+                   help="uniformly random index bytes and codebooks instead of quantized "
+                        "N(0, 0.02) weights (same kernels and bytes; for profiled runs, where "
+                        "the quantile/argmin generator's many small launches are slow)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also time a plain 1 GiB device copy (the yardstick that scales "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -95,7 +99,12 @@ class Mat:
         self.bytes = synth.layer_bytes(N, K, NE, BS, 1, x_bytes=2, y_bytes=4)
 
 
-def build_model(dev, n_layers):
+def _make(random_weights):
+    from nativebit_amd import synth
+    return synth.make_random_layer if random_weights else synth.make_layer
+
+
+def build_model(dev, n_layers, random_weights=False):
     """182 packed layers generated on the GPU.  q|k|v and gate|up of a layer
     live in one buffer each (rows never share a block when K % 128 == 0, so
     the concatenation is byte-identical to one fused packed layer, as the
@@ -105,7 +114,7 @@ def build_model(dev, n_layers):
     layers = []
     t0 = time.time()
     for l in range(n_layers):
-        gen = {name: synth.make_layer(N, K, NE, BS, seed=l * 7 + j, device=dev)
+        gen = {name: _make(random_weights)(N, K, NE, BS, seed=l * 7 + j, device=dev)
                for j, (name, N, K) in enumerate(synth.LAYER_SHAPES)}
         mats = {}
         for group in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
@@ -292,10 +301,10 @@ PREFILL_SHAPES = (("qkv", 7680, 2560), ("o", 2560, 2560), ("gate|up", 13824, 256
                   ("down", 2560, 6912))
 
 
-def bench_prefill(dev):
+def bench_prefill(dev, random_weights=False):
     """Config 4a: prefill-sized contraction with the packed weights."""
     from nativebit_amd import ops, synth
-    layers = {n: synth.make_layer(N, K, seed=50 + i, device=dev)
+    layers = {n: _make(random_weights)(N, K, seed=50 + i, device=dev)
               for i, (n, N, K) in enumerate(PREFILL_SHAPES)}
     out = {}
     for M in (512, 2048):
@@ -414,7 +423,7 @@ def main():
     log(f"[bench] {torch.cuda.get_device_name(dev)} {props.gcnArchName} "
         f"CUs={props.multi_processor_count}")
 
-    layers = build_model(dev, args.layers)
+    layers = build_model(dev, args.layers, args.random_weights)
     all_mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
     step_bytes = sum(m.bytes for m in all_mats)
     wanted = args.schedules.split(",")
@@ -503,7 +512,7 @@ def main():
         extra = {}
         wanted_extra = [e for e in args.extra.split(",") if e]
         for name, fn in (("decode", lambda: bench_decode(dev)),
-                         ("prefill", lambda: bench_prefill(dev)),
+                         ("prefill", lambda: bench_prefill(dev, args.random_weights)),
                          ("skinny", lambda: bench_skinny(dev, layers)),
                          ("sweep", lambda: bench_sweep(dev))):
             if name not in wanted_extra:

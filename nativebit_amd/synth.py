@@ -106,6 +106,23 @@ def make_layer(out_features: int, in_features: int, n_entries: int = 8,
                        cb.contiguous(), packed, idx if keep_indices else None)
 
 
+def make_random_layer(out_features: int, in_features: int, n_entries: int = 8,
+                      block_size: int = 128, seed: int = 0, device="cpu",
+                      std: float = 0.02) -> PackedLayer:
+    """A layer of the same format with uniformly random index bytes and
+    N(0, std^2) codebooks -- no quantile or argmin pass, so it is cheap to
+    make on a profiled device (the kernels do the same work for any bytes)."""
+    device = torch.device(device)
+    gen = torch.Generator(device=device).manual_seed(int(seed))
+    total = out_features * in_features
+    nb = -(-total // block_size)
+    bits = host_pack.bits_for_entries(n_entries)
+    packed = torch.randint(0, 256, (host_pack.packed_nbytes(nb * block_size, bits),),
+                           generator=gen, device=device, dtype=torch.uint8)
+    cb = torch.randn(nb, n_entries, generator=gen, device=device) * std
+    return PackedLayer(out_features, in_features, n_entries, block_size, bits, cb, packed, None)
+
+
 def make_activation(k: int, m: int = 1, seed: int = 1000, device="cpu",
                     dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """x ~ N(0, 1) of shape (m, k), drawn in fp32 then cast."""
