@@ -21,6 +21,10 @@ same buffers, each captured once in a HIP graph and replayed:
 per replay.  The other two are reported beside it.  The other BASELINE
 configurations are reported in the same JSON line under "configs":
 
+  config0  config 0: one 6912x2560 layer, x fp32 (the reference's exact fp32
+           arithmetic), one nb_gemv launch per matvec over rotated copies,
+           beside the reference CPU torch path on the same layer
+
   decode   config 4b: random-init 2.2B packed model (vocab 32000), greedy,
            128 prompt + 256 generated tokens, tokens/s of the generation
            (nativebit_amd.decode: one HIP graph per token)
@@ -35,7 +39,7 @@ configurations are reported in the same JSON line under "configs":
            copies rotated over > 512 MB so no cache holds them)
 
 Usage: python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-extra] [--extra decode,prefill,skinny,sweep]
+                       [--no-extra] [--extra config0,decode,prefill,skinny,sweep]
 """
 from __future__ import annotations
 
@@ -77,7 +81,7 @@ def parse():
                    help="CPU baseline passes continue until this much time has been spent")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the decode / prefill / skinny / sweep configurations")
-    p.add_argument("--extra", default="decode,prefill,skinny,sweep",
+    p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep",
                    help="comma list of extra configurations to run")
     p.add_argument("--random-weights", action="store_true",
                    help="uniformly random index bytes and codebooks instead of quantized "
@@ -374,6 +378,50 @@ def bench_skinny(dev, layers):
     return out
 
 
+def bench_config0(dev, cpu=True):
+    """Config 0: one packed 6912x2560 layer (NE 8, BS 128, quantized N(0, 0.02)
+    weights), x fp32 N(0, 1), batch 1 -- nb_gemv with the reference's exact
+    fp32 arithmetic (gemv_fast_kernel), one launch per matvec, each timed
+    launch reading a different copy of the layer (> 512 MB in all); beside
+    it the reference CPU torch path on the same layer."""
+    from nativebit_amd import ops, synth
+    N, K = 6912, 2560
+    lay = synth.make_layer(N, K, NE, BS, seed=0, device=dev)
+    per = synth.layer_bytes(N, K, NE, BS, 1, x_bytes=4, y_bytes=4)
+    copies = max(2, -(-(512 << 20) // per))
+    ps = [lay.packed.clone() for _ in range(copies)]
+    cbs = [lay.codebook.clone() for _ in range(copies)]
+    x = synth.make_activation(K, seed=1000, device=dev)[0].contiguous()
+    y = torch.empty(1, N, device=dev)
+
+    def run():
+        for p, c in zip(ps, cbs):
+            ops.gemv(x, p, c, N, K, out=y)
+    ms = graph_time(run, 10, 3) / copies
+    out = {"us": round(ms * 1e3, 2), "GB_s": round(per / ms / 1e6, 1),
+           "pct_hbm_peak": round(per / ms / 1e6 / HBM_PEAK_GBS * 100, 2), "bytes": per,
+           "copies": copies, "kernel": "gemv_fast_kernel (fp32 x, exact fp32 codebook values)"}
+    if cpu:
+        from oracle import oracle as O
+        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        torch.set_num_threads(threads)
+        xh, ph, ch = x.cpu(), lay.packed.cpu(), lay.codebook.cpu()
+        O.torch_packed_linear_f32(xh, ph, ch, N, K, BS, BITS)
+        times = []
+        t_start = time.perf_counter()
+        while len(times) < 5 or time.perf_counter() - t_start < 3.0:
+            t0 = time.perf_counter()
+            O.torch_packed_linear_f32(xh, ph, ch, N, K, BS, BITS)
+            times.append(time.perf_counter() - t0)
+        t = statistics.median(times)
+        out["cpu_reference_path"] = {"us": round(t * 1e6, 1), "GB_s": round(per / t / 1e9, 3),
+                                     "threads": threads, "passes": len(times),
+                                     "what": "torch CPU unpack + gather + F.linear "
+                                             "(triton_kernel.py:258-275)"}
+    del ps, cbs
+    return out
+
+
 def bench_sweep(dev):
     """Config 3: bit width x block size at batch 1 (nb_gemv)."""
     from nativebit_amd import ops, synth
@@ -511,7 +559,8 @@ def main():
     if not args.no_extra:
         extra = {}
         wanted_extra = [e for e in args.extra.split(",") if e]
-        for name, fn in (("decode", lambda: bench_decode(dev)),
+        for name, fn in (("config0", lambda: bench_config0(dev, not args.no_cpu_baseline)),
+                         ("decode", lambda: bench_decode(dev)),
                          ("prefill", lambda: bench_prefill(dev, args.random_weights)),
                          ("skinny", lambda: bench_skinny(dev, layers)),
                          ("sweep", lambda: bench_sweep(dev))):
