@@ -459,6 +459,68 @@ def test_batched_fused_forms(dev):
         assert rel(y.cpu(), refs[i]) <= REL_F32, (i, rel(y.cpu(), refs[i]))
 
 
+def test_batched_many_small_fused_items(dev):
+    """Many small items, so one workgroup forms several problems'
+    activations (each RMSNorm with its own barriers) and takes chunks of
+    several problems: every item equals its unfused sequence."""
+    g = torch.Generator().manual_seed(99)
+    eps = 1e-6
+    items, plain, adds = [], [], []
+    for i in range(40):
+        N, K = (17 + 13 * i) % 300 + 1, 128 * (1 + i % 5)
+        mode = ("rmsnorm", "silu_mul", "bf16")[i % 3]
+        yf = "add" if i % 2 else "store"
+        idx, p, cb = random_layer(N, K, 3, 8, 128, 2000 + i)
+        pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+        form = {"y": yf}
+        if mode == "rmsnorm":
+            x = torch.randn(K, generator=g)
+            w = 1 + 0.1 * torch.randn(K, generator=g)
+            form["x"] = ("rmsnorm", w.to(dev), eps)
+            a = _fused_activations(mode, x, w, eps)
+        elif mode == "silu_mul":
+            x = torch.randn(2 * K, generator=g)
+            form["x"] = "silu_mul"
+            a = _fused_activations(mode, x)
+        else:
+            x = torch.randn(K, generator=g).to(torch.bfloat16)
+            a = x
+        y0 = torch.randn(N, generator=g) if yf == "add" else torch.zeros(N)
+        y = y0.clone().to(dev) if yf == "add" else torch.full((N,), float("nan"), device=dev)
+        items.append((x.to(dev), pt, ct, y, N, K, form))
+        plain.append((a.to(dev), pt, ct, torch.empty(N, device=dev), N, K))
+        adds.append(y0)
+    note("40 small fused items in one batch")
+    ops.GemvBatch(items).run()
+    ops.GemvBatch(plain).run()
+    for i, (item, pl) in enumerate(zip(items, plain)):
+        unfused = pl[3].cpu() + adds[i]
+        assert rel(item[3].cpu(), unfused) <= 1e-3, (i, rel(item[3].cpu(), unfused))
+
+
+def test_skinny_batched_more_items_than_one_launch(dev):
+    """More items than one skinny launch takes (512): the launcher splits
+    the table; every item still equals its own GEMV."""
+    M, n = 3, 600
+    items, refs = [], []
+    for i in range(n):
+        N, K = 1 + (i * 37) % 200, 128 * (1 + i % 3)
+        idx, p, cb = random_layer(N, K, 3, 8, 128, 3000 + i)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(i)).to(torch.bfloat16)
+        items.append((x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev),
+                      torch.full((M, N), float("nan"), device=dev), N, K))
+        refs.append((idx, cb, x))
+    note(f"skinny M={M} with {n} items")
+    ops.GemvBatch(items, m=M).run()
+    torch.cuda.synchronize()
+    for i in range(0, n, 7):  # a spread sample against the fp64 brute force
+        idx, cb, x = refs[i]
+        N, K = items[i][4], items[i][5]
+        ref = ref_gemv(x, idx, cb, 128, N, K)
+        assert rel(items[i][3].cpu(), ref) <= REL_F32, (i, N, K)
+    assert all(torch.isfinite(it[3]).all().item() for it in items)
+
+
 def test_batched_add_twice_accumulates(dev):
     """y_mode add reads y each launch: two runs add the product twice."""
     N, K = 2560, 2560
