@@ -34,12 +34,15 @@ configurations are reported in the same JSON line under "configs":
   skinny   config 2: M = 1, 2, 4, 8, 16 activation rows over all 182 matmuls,
            one batched launch per step (nb_gemm_skinny_batched at M > 1),
            beside 182 per-matmul nb_gemv launches
+  quantize nb_quantize_pack: nearest-entry quantization straight into the
+           3-bit stream for one 6912x2560 layer (GB/s), beside the
+           reference's distance-tensor formulation on the GPU
   sweep    config 3: nb_gemv at batch 1, NE in {4, 8, 16} x BS in {64, 128,
            256} on 6912x2560 and 2560x6912 (random indices and codebooks;
            copies rotated over > 512 MB so no cache holds them)
 
 Usage: python bench.py [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--no-extra] [--extra config0,decode,prefill,skinny,sweep]
+                       [--no-extra] [--extra config0,decode,prefill,skinny,sweep,quantize]
 """
 from __future__ import annotations
 
@@ -81,7 +84,7 @@ def parse():
                    help="CPU baseline passes continue until this much time has been spent")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the decode / prefill / skinny / sweep configurations")
-    p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep",
+    p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep,quantize",
                    help="comma list of extra configurations to run")
     p.add_argument("--random-weights", action="store_true",
                    help="uniformly random index bytes and codebooks instead of quantized "
@@ -422,6 +425,27 @@ def bench_config0(dev, cpu=True):
     return out
 
 
+def bench_quantize(dev):
+    """Quantize-at-pack on the GPU (SURVEY next row 4): nearest-entry
+    indices of a 6912x2560 fp32 weight against its per-block quantile
+    codebooks, packed to the 3-bit stream by one kernel (nb_quantize_pack),
+    beside the reference's formulation on the same device (a dense
+    blocks x block_size x entries distance tensor, argmin, then nb_pack)."""
+    from nativebit_amd import ops, synth
+    N, K = 6912, 2560
+    g = torch.Generator(device=dev).manual_seed(11)
+    w = torch.randn(N * K, generator=g, device=dev) * 0.02
+    cb = synth.block_codebooks(w, N * K, NE, BS)
+    nbytes = w.numel() * 4 + cb.numel() * 4 + ops.packed_nbytes(N * K, BITS)
+    ms = event_time(lambda: ops.quantize_pack(w, cb, BS), 20)
+    ms_ref = event_time(lambda: ops.pack(synth.nearest_indices(w, N * K, cb, BS), BITS), 5)
+    return {"us": round(ms * 1e3, 1), "GB_s": round(nbytes / ms / 1e6, 1),
+            "pct_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 1), "bytes": nbytes,
+            "torch_distance_argmin_then_pack_us": round(ms_ref * 1e3, 1),
+            "bit_exact_vs_torch_path": bool(torch.equal(
+                ops.quantize_pack(w, cb, BS), ops.pack(synth.nearest_indices(w, N * K, cb, BS), BITS)))}
+
+
 def bench_sweep(dev):
     """Config 3: bit width x block size at batch 1 (nb_gemv)."""
     from nativebit_amd import ops, synth
@@ -563,7 +587,8 @@ def main():
                          ("decode", lambda: bench_decode(dev)),
                          ("prefill", lambda: bench_prefill(dev, args.random_weights)),
                          ("skinny", lambda: bench_skinny(dev, layers)),
-                         ("sweep", lambda: bench_sweep(dev))):
+                         ("sweep", lambda: bench_sweep(dev)),
+                         ("quantize", lambda: bench_quantize(dev))):
             if name not in wanted_extra:
                 continue
             t0 = time.time()

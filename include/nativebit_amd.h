@@ -127,6 +127,19 @@ int nb_unpack(const uint8_t* packed, uint8_t* idx_out, int64_t count, int bits,
 int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits,
             void* stream);
 
+/* Quantize-at-pack: the nearest codebook entry of each of the `total`
+ * flat fp32 weights w, by squared distance in fp32 with the first entry on
+ * ties, written straight into the LSB-first stream at `bits` per index
+ * (nb_packed_nbytes(num_blocks * block_size, bits) bytes, as nb_pack).
+ * codebook is num_blocks x n_entries fp32; the last block's padding
+ * (weights total .. num_blocks * block_size - 1) counts as 0.0, and
+ * block_size must be ceil(total / num_blocks).  Replaces quantize_weight
+ * (inference/pack.py:21-35) + pack_indices_3bit (38-57) without the
+ * reference's (blocks x block_size x entries) distance tensor.  Inputs are
+ * finite. */
+int nb_quantize_pack(const float* w, int64_t total, const float* codebook, int64_t num_blocks,
+                     int n_entries, int block_size, int bits, uint8_t* packed_out, void* stream);
+
 /*
  * Dequantize the first `total` weights: w[i] = codebook[i / block_size][index
  * i], written as float32 (exact copy) or bfloat16 (round to nearest even, as

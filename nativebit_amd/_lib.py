@@ -54,6 +54,7 @@ SIGNATURES = {
     "nb_unpack": (_I, [_P, _P, _L, _I, _P]),
     "nb_pack": (_I, [_P, _P, _L, _I, _P]),
     "nb_dequant": (_I, [_P, _P, _P, _I, _L, _L, _I, _I, _I, _P]),
+    "nb_quantize_pack": (_I, [_P, _L, _P, _L, _I, _I, _I, _P, _P]),
     "nb_gemv_batch_table_bytes": (_L, [_I]),
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),

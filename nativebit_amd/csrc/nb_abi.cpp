@@ -6,6 +6,7 @@
 // (inference/triton_kernel.py:244-257), each failure returns a distinct
 // status with a message and nothing is launched.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -179,6 +180,30 @@ int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits, vo
     int st = ensure_device();
     if (st) return st;
     return launch_pack(idx, packed_out, count, bits, static_cast<hipStream_t>(stream));
+}
+
+int nb_quantize_pack(const float* w, int64_t total, const float* codebook, int64_t num_blocks,
+                     int n_entries, int block_size, int bits, uint8_t* packed_out, void* stream) {
+    const char* fn = "nb_quantize_pack";
+    if (bits < 1 || bits > 8) return fail(NB_EUNSUPPORTED, "%s: bits=%d outside 1..8", fn, bits);
+    if (n_entries < 1 || n_entries > (1 << bits)) {
+        return fail(NB_EINVAL, "%s: n_entries=%d outside 1..2^bits", fn, n_entries);
+    }
+    if (block_size < 1) return fail(NB_EINVAL, "%s: block_size=%d < 1", fn, block_size);
+    if (total < 0 || num_blocks < 0) return fail(NB_EINVAL, "%s: negative size", fn);
+    if (num_blocks > (INT64_MAX / 2) / block_size) return fail(NB_EINVAL, "%s: size overflow", fn);
+    // the layout of quantize_weight: block_size = ceil(total / num_blocks)
+    if (num_blocks * block_size < total || (total > 0 && (num_blocks - 1) * block_size >= total)) {
+        return fail(NB_EINVAL, "%s: %lld blocks of %d do not tile %lld weights", fn,
+                    (long long)num_blocks, block_size, (long long)total);
+    }
+    if (total == 0) return NB_OK;
+    if (!w || !codebook || !packed_out) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(w, 4) || !aligned(codebook, 4)) return fail(NB_EALIGN, "%s: w/codebook not 4-byte aligned", fn);
+    int st = ensure_device();
+    if (st) return st;
+    return launch_quantize_pack(w, total, codebook, num_blocks, n_entries, block_size, bits,
+                                packed_out, static_cast<hipStream_t>(stream));
 }
 
 int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out, int w_dtype,

@@ -6,7 +6,8 @@
 //
 // Reference semantics: nativebit/pack.py:21-169 (pack_3bit, unpack_3bit,
 // pack_4bit, unpack_4bit, pack_nbits, unpack_nbits, reconstruct_weight),
-// inference/triton_kernel.py:199-220 (pack_indices_to_3bit).
+// inference/triton_kernel.py:199-220 (pack_indices_to_3bit),
+// inference/pack.py:21-35 (quantize_weight, fused here with the pack).
 #include "nb_device.h"
 #include "nb_internal.h"
 
@@ -56,6 +57,85 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
     }
 }
 
+// Nearest codebook entry of flat weight i: squared distance (w - c)^2 to
+// each entry of its block's codebook in fp32, the first index on ties
+// (strict <, as numpy's and torch's argmin); weights at or past `total`
+// (the padded tail of the last block) are 0.0.  Inputs are finite.
+__device__ __forceinline__ uint32_t nearest_entry(const float* __restrict__ w, int64_t total,
+                                                  const float* __restrict__ cb, int n_entries,
+                                                  int block_size, int64_t i) {
+    const float v = i < total ? w[i] : 0.f;
+    const float* c = cb + (i / block_size) * n_entries;
+    float d = v - c[0];
+    float best_d = d * d;
+    uint32_t best = 0;
+    for (int e = 1; e < n_entries; ++e) {
+        d = v - c[e];
+        const float dd = d * d;
+        if (dd < best_d) {
+            best_d = dd;
+            best = (uint32_t)e;
+        }
+    }
+    return best;
+}
+
+// Quantize-at-pack: one thread per group of 8 indices, i.e. `bits` whole
+// bytes of the LSB-first stream (8 fields of `bits` bits), each field the
+// weight's nearest entry, so the (blocks x block_size x entries) distance
+// tensor of the reference's quantize_weight never exists
+// (inference/pack.py:21-35).  Up to 16 entries the block's codebook stays in
+// registers while consecutive indices share a block; NE (4, 8 or 16, else
+// 0 = any count up to 16) fixes the compare loop's length.
+template <bool kSmallNE, int NE>
+__global__ __launch_bounds__(kThreads) void quantize_pack_kernel(
+    const float* __restrict__ w, int64_t total, const float* __restrict__ cb, int n_entries,
+    int block_size, int64_t count, int bits, uint8_t* __restrict__ out, int64_t nbytes) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    const int64_t groups = (count + 7) / 8;
+    for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < groups; t += stride) {
+        float c[16];
+        int64_t cur_block = -1;
+        uint64_t acc = 0;  // 8 fields, LSB first (8 * bits <= 64)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int64_t i = 8 * t + j;
+            uint32_t f = 0;
+            if (i < count) {
+                if (kSmallNE) {
+                    const float v = i < total ? w[i] : 0.f;
+                    const int64_t blk = i / block_size;
+                    constexpr int kE = NE ? NE : 16;
+                    if (blk != cur_block) {
+                        cur_block = blk;
+#pragma unroll
+                        for (int e = 0; e < kE; ++e) c[e] = e < n_entries ? cb[blk * n_entries + e] : 0.f;
+                    }
+                    float d = v - c[0];
+                    float best_d = d * d;
+#pragma unroll
+                    for (int e = 1; e < kE; ++e) {
+                        d = v - c[e];
+                        const float dd = d * d;
+                        if ((NE || e < n_entries) && dd < best_d) {
+                            best_d = dd;
+                            f = (uint32_t)e;
+                        }
+                    }
+                } else {
+                    f = nearest_entry(w, total, cb, n_entries, block_size, i);
+                }
+            }
+            acc |= (uint64_t)f << (j * bits);
+        }
+        // bytes bits * t .. bits * t + bits - 1 of the stream
+        for (int k = 0; k < bits; ++k) {
+            const int64_t ob = (int64_t)bits * t + k;
+            if (ob < nbytes) out[ob] = (uint8_t)(acc >> (8 * k));
+        }
+    }
+}
+
 template <bool kBF16>
 __global__ __launch_bounds__(kThreads) void dequant_kernel(
     const uint8_t* __restrict__ packed, int64_t nbytes,
@@ -94,6 +174,31 @@ int launch_pack(const uint8_t* idx, uint8_t* out, int64_t count, int bits,
     hipLaunchKernelGGL(pack_kernel, dim3(grid_for(nbytes)), dim3(kThreads), 0,
                        stream, idx, count, bits, out, nbytes);
     return check_launch("nb_pack");
+}
+
+int launch_quantize_pack(const float* w, int64_t total, const float* codebook,
+                         int64_t num_blocks, int n_entries, int block_size, int bits,
+                         uint8_t* out, hipStream_t stream) {
+    const int64_t count = num_blocks * block_size;
+    const int64_t nbytes = packed_nbytes(count, bits);
+    if (nbytes == 0) return NB_OK;
+    const int grid = grid_for((count + 7) / 8);
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, w, total, codebook,
+                           n_entries, block_size, count, bits, out, nbytes);
+    };
+    switch (n_entries) {
+        case 4: go(quantize_pack_kernel<true, 4>); break;
+        case 8: go(quantize_pack_kernel<true, 8>); break;
+        case 16: go(quantize_pack_kernel<true, 16>); break;
+        default:
+            if (n_entries < 16) {
+                go(quantize_pack_kernel<true, 0>);
+            } else {
+                go(quantize_pack_kernel<false, 0>);
+            }
+    }
+    return check_launch("nb_quantize_pack");
 }
 
 int launch_dequant(const uint8_t* packed, const float* codebook, void* w,

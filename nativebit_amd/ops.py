@@ -12,6 +12,7 @@ import math
 import torch
 
 from . import _lib
+from . import pack as host_pack
 
 _DT = {torch.float32: _lib.NB_F32, torch.bfloat16: _lib.NB_BF16}
 
@@ -88,6 +89,33 @@ def gemv(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
         out.data_ptr(), _DT[out_dtype], out.stride(0) if M > 1 else N,
         M, N, K, bits, n_entries, block_size, _stream(x)))
     return out.reshape(N) if squeeze else out
+
+
+def quantize_pack(w: torch.Tensor, codebook: torch.Tensor, block_size: int,
+                  bits: int | None = None) -> torch.Tensor:
+    """Nearest-entry indices of the flat weights ``w`` against per-block
+    ``codebook`` (num_blocks, n_entries), first entry on ties, packed
+    LSB-first (quantize_weight + pack_indices_3bit, inference/pack.py:21-57)
+    by one kernel: uint8 stream of packed_nbytes(num_blocks * block_size,
+    bits) bytes."""
+    for name, t in (("w", w), ("codebook", codebook)):
+        _require_cuda(name, t)
+    _same_device(w, codebook)
+    if w.dtype != torch.float32 or codebook.dtype != torch.float32:
+        raise TypeError("w and codebook must be float32")
+    if codebook.dim() != 2:
+        raise ValueError("codebook must be (num_blocks, n_entries)")
+    w = w.contiguous().reshape(-1)
+    codebook = codebook.contiguous()
+    num_blocks, n_entries = codebook.shape
+    if bits is None:
+        bits = host_pack.bits_for_entries(n_entries)
+    out = torch.empty(packed_nbytes(num_blocks * block_size, bits), dtype=torch.uint8,
+                      device=w.device)
+    _lib.check(_lib.load().nb_quantize_pack(w.data_ptr(), w.numel(), codebook.data_ptr(),
+                                            num_blocks, n_entries, block_size, bits,
+                                            out.data_ptr(), _stream(w)))
+    return out
 
 
 class GemvBatch:

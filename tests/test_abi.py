@@ -190,6 +190,23 @@ def test_batch_fused_forms_validation():
     assert batched(_lib.NB_BF16, *base, 0, Y, None, 0.0, 0) == _lib.NB_EUNSUPPORTED
 
 
+def test_quantize_pack_validation():
+    """nb_quantize_pack: format and tiling checks on the host."""
+    q = _lib.load().nb_quantize_pack
+    ok = (FAKE, 1000, FAKE, 8, 8, 125, 3, FAKE, None)
+    assert q(*ok[:1], 0, FAKE, 0, 8, 125, 3, FAKE, None) == _lib.NB_OK      # nothing to do
+    for i, bad, st in ((6, 0, _lib.NB_EUNSUPPORTED), (6, 9, _lib.NB_EUNSUPPORTED),   # bits
+                       (4, 9, _lib.NB_EINVAL), (4, 0, _lib.NB_EINVAL),               # entries > 2^bits
+                       (5, 0, _lib.NB_EINVAL),                                        # block size
+                       (3, 7, _lib.NB_EINVAL), (3, 9, _lib.NB_EINVAL),               # blocks don't tile
+                       (1, -1, _lib.NB_EINVAL),
+                       (0, None, _lib.NB_EINVAL), (7, None, _lib.NB_EINVAL),
+                       (0, FAKE + 2, _lib.NB_EALIGN)):
+        a = list(ok)
+        a[i] = bad
+        assert q(*a) == st, (i, bad)
+
+
 def test_skinny_batch_validation():
     """nb_gemm_skinny_batched: M range, bf16 activations only, the shared
     item checks and the y_dtype / NB_Y_ADD rules, all on the host."""

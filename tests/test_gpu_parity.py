@@ -82,6 +82,45 @@ def test_dequant_bit_exact(dev, N, K, bits, ne, bs):
     assert torch.equal(w16.cpu(), torch.from_numpy(ref).to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("total,ne,bs,bits", [
+    (6912 * 2560, 8, 128, 3), (1000, 8, 125, 3), (1001, 8, 128, 3), (777, 4, 64, 2),
+    (4096, 16, 256, 4), (333, 5, 7, 3), (100, 2, 10, 1), (515, 200, 64, 8), (64, 8, 128, 3),
+])
+def test_quantize_pack_bit_exact(dev, total, ne, bs, bits):
+    """GPU quantize-at-pack equals the oracle's quantize_weight restatement
+    packed by the oracle, byte for byte -- with planted exact ties (weights
+    at the midpoint of two entries, and equal entries) that must take the
+    first index, and a padded tail block."""
+    note(f"quantize_pack total={total} ne={ne} bs={bs} bits={bits}")
+    rng = np.random.default_rng(total + ne)
+    nb = -(-total // bs)
+    w = (rng.standard_normal(total) * 0.02).astype(np.float32)
+    cb = np.sort((rng.standard_normal((nb, ne)) * 0.02).astype(np.float32), axis=1)
+    if ne >= 3:
+        cb[::3, 1] = cb[::3, 2]                      # duplicate entries: first wins
+    # midpoints of entries 0 and 1, exactly representable distance ties
+    for i in range(0, total, 17):
+        b = i // bs
+        lo, hi = np.float32(cb[b, 0]), np.float32(cb[b, 1])
+        w[i] = np.float32((lo + hi) / np.float32(2))
+    ref = O.pack(O.quantize(w, cb, bs), bits)
+    got = ops.quantize_pack(torch.from_numpy(w).to(dev), torch.from_numpy(cb).to(dev), bs, bits)
+    assert got.numel() == ref.size
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_quantize_pack_roundtrip_synth(dev):
+    """The synthetic generator's torch quantization (squared distance argmin,
+    per-block quantile codebooks) packed by nb_pack equals nb_quantize_pack
+    on the same weights and codebooks."""
+    N, K = 2560, 2560
+    g = torch.Generator(device=dev).manual_seed(5)
+    w = torch.randn(N * K, generator=g, device=dev) * 0.02
+    cb = synth.block_codebooks(w, N * K, 8, 128)
+    idx = synth.nearest_indices(w, N * K, cb, 128)
+    assert torch.equal(ops.quantize_pack(w, cb, 128), ops.pack(idx, 3))
+
+
 def test_reference_gather_equals_dequant(dev):
     """The reference's own torch unpack+gather (restated) equals nb_dequant."""
     N, K = 300, 2560
