@@ -443,7 +443,21 @@ def bench_quantize(dev):
             "pct_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 1), "bytes": nbytes,
             "torch_distance_argmin_then_pack_us": round(ms_ref * 1e3, 1),
             "bit_exact_vs_torch_path": bool(torch.equal(
-                ops.quantize_pack(w, cb, BS), ops.pack(synth.nearest_indices(w, N * K, cb, BS), BITS)))}
+                ops.quantize_pack(w, cb, BS), ops.pack(synth.nearest_indices(w, N * K, cb, BS), BITS))),
+            "codebooks": bench_codebooks(w, N * K)}
+
+
+def bench_codebooks(w, total):
+    """Per-block quantile codebooks on the GPU (nb_block_codebooks: one
+    64-lane workgroup sorts each block in LDS) beside torch.quantile over the
+    same blocks on the same device, both timed with events."""
+    from nativebit_amd import ops, synth
+    ms = event_time(lambda: ops.block_codebooks(w, NE, BS), 10)
+    ms_ref = event_time(lambda: synth.block_codebooks(w, total, NE, BS), 3)
+    return {"us": round(ms * 1e3, 1), "GB_s_read": round(total * 4 / ms / 1e6, 1),
+            "torch_quantile_us": round(ms_ref * 1e3, 1),
+            "bit_exact_vs_torch_quantile": bool(torch.equal(
+                ops.block_codebooks(w, NE, BS), synth.block_codebooks(w, total, NE, BS)))}
 
 
 def bench_sweep(dev):

@@ -127,6 +127,21 @@ int nb_unpack(const uint8_t* packed, uint8_t* idx_out, int64_t count, int bits,
 int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits,
             void* stream);
 
+/* Per-block quantile codebooks (the codebook init of a packed layer):
+ * codebook_out[b][e] = quantile(w[b*block_size .. min((b+1)*block_size,
+ * total)), q_e), q = linspace(0, 1, n_entries), linear interpolation -- as
+ * torch.quantile in init_codebook_percentile (nativebit/codebook_utils.py:
+ * 6-22), called per block by NativeBitLinear (nativebit/layers.py:76); the
+ * last block takes only the weights that exist.  ceil(total / block_size)
+ * x n_entries fp32 outputs; block_size <= 1024, n_entries <= 256; inputs
+ * finite. */
+int nb_block_codebooks(const float* w, int64_t total, int block_size, int n_entries,
+                       float* codebook_out, void* stream);
+
+/* The n (1..256) fractions nb_block_codebooks uses: torch.linspace(0, 1, n)
+ * in fp32 (host only, for callers and tests). */
+int nb_linspace01(int n, float* out);
+
 /* Quantize-at-pack: the nearest codebook entry of each of the `total`
  * flat fp32 weights w, by squared distance in fp32 with the first entry on
  * ties, written straight into the LSB-first stream at `bits` per index

@@ -55,6 +55,8 @@ SIGNATURES = {
     "nb_pack": (_I, [_P, _P, _L, _I, _P]),
     "nb_dequant": (_I, [_P, _P, _P, _I, _L, _L, _I, _I, _I, _P]),
     "nb_quantize_pack": (_I, [_P, _L, _P, _L, _I, _I, _I, _P, _P]),
+    "nb_block_codebooks": (_I, [_P, _L, _I, _I, _P, _P]),
+    "nb_linspace01": (_I, [_I, _P]),
     "nb_gemv_batch_table_bytes": (_L, [_I]),
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),

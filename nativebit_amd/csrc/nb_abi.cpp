@@ -182,6 +182,52 @@ int nb_pack(const uint8_t* idx, uint8_t* packed_out, int64_t count, int bits, vo
     return launch_pack(idx, packed_out, count, bits, static_cast<hipStream_t>(stream));
 }
 
+// torch.linspace(0, 1, n) in fp32 as torch's kernel forms it: step =
+// 1 / (n - 1); the first half counts up from 0, the second half down from
+// 1, each value one fused multiply-add (single rounding).
+static void linspace01(int n, float* q) {
+    if (n == 1) {
+        q[0] = 0.f;
+        return;
+    }
+    const float step = 1.0f / (float)(n - 1);
+    const int halfway = n / 2;
+    for (int i = 0; i < n; ++i) {
+        q[i] = i < halfway ? std::fma(step, (float)i, 0.0f)
+                           : std::fma(-step, (float)(n - i - 1), 1.0f);
+    }
+}
+
+int nb_block_codebooks(const float* w, int64_t total, int block_size, int n_entries,
+                       float* codebook_out, void* stream) {
+    const char* fn = "nb_block_codebooks";
+    if (block_size < 1 || block_size > 1024) {
+        return fail(NB_EUNSUPPORTED, "%s: block_size=%d outside 1..1024", fn, block_size);
+    }
+    if (n_entries < 1 || n_entries > 256) {
+        return fail(NB_EUNSUPPORTED, "%s: n_entries=%d outside 1..256", fn, n_entries);
+    }
+    if (total < 0) return fail(NB_EINVAL, "%s: total=%lld < 0", fn, (long long)total);
+    if (total == 0) return NB_OK;
+    if (!w || !codebook_out) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(w, 4) || !aligned(codebook_out, 4)) {
+        return fail(NB_EALIGN, "%s: w/codebook not 4-byte aligned", fn);
+    }
+    int st = ensure_device();
+    if (st) return st;
+    float q[256];
+    linspace01(n_entries, q);
+    const int64_t num_blocks = (total + block_size - 1) / block_size;
+    return launch_block_codebooks(w, total, num_blocks, block_size, n_entries, q, codebook_out,
+                                  static_cast<hipStream_t>(stream));
+}
+
+int nb_linspace01(int n, float* out) {
+    if (n < 1 || n > 256 || !out) return fail(NB_EINVAL, "nb_linspace01: n=%d", n);
+    linspace01(n, out);
+    return NB_OK;
+}
+
 int nb_quantize_pack(const float* w, int64_t total, const float* codebook, int64_t num_blocks,
                      int n_entries, int block_size, int bits, uint8_t* packed_out, void* stream) {
     const char* fn = "nb_quantize_pack";

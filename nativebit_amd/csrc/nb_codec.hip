@@ -8,6 +8,8 @@
 // pack_4bit, unpack_4bit, pack_nbits, unpack_nbits, reconstruct_weight),
 // inference/triton_kernel.py:199-220 (pack_indices_to_3bit),
 // inference/pack.py:21-35 (quantize_weight, fused here with the pack).
+#include <math.h>
+
 #include "nb_device.h"
 #include "nb_internal.h"
 
@@ -136,6 +138,68 @@ __global__ __launch_bounds__(kThreads) void quantize_pack_kernel(
     }
 }
 
+// Per-block quantile codebooks: cb[b][e] = quantile(w_block, q_e) with
+// linear interpolation, as torch.quantile(w_block, linspace(0, 1, NE))
+// (nativebit/codebook_utils.py:6-22, called per block by
+// nativebit/layers.py:76): sort the block, rank = q_e * (n - 1) in fp32,
+// lower = (int) rank, upper = ceil(rank), weight = rank - lower, and
+// torch's lerp, which rounds once: fma(weight, hi - lo, lo) for weight < 0.5,
+// else fma(weight - 1, hi - lo, hi).  The last block takes only the weights
+// that exist (n = total - first).  One 64-lane workgroup per block: the
+// block is sorted in LDS by a bitonic network over the next power of two
+// (+inf padding), every compare-exchange of a pass on its own lane, a
+// barrier between passes.  Inputs are finite.
+constexpr int kCbMaxBlock = 1024;
+constexpr int kCbMaxEntries = 256;
+struct QuantileFractions {
+    float q[kCbMaxEntries];
+};
+
+__global__ __launch_bounds__(64) void block_codebooks_kernel(
+    const float* __restrict__ w, int64_t total, int64_t num_blocks, int block_size, int n_entries,
+    QuantileFractions qf, float* __restrict__ cb) {
+    __shared__ float v[kCbMaxBlock];
+    const int lane = threadIdx.x;
+    for (int64_t b = blockIdx.x; b < num_blocks; b += gridDim.x) {
+        const int64_t first = b * block_size;
+        const int n = (int)min((int64_t)block_size, total - first);
+        int P = 1;
+        while (P < n) P <<= 1;
+        for (int i = lane; i < P; i += 64) v[i] = i < n ? w[first + i] : INFINITY;
+        __syncthreads();
+        for (int k = 2; k <= P; k <<= 1) {
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                for (int t = lane; t < P / 2; t += 64) {
+                    // pair (i, i + j) of pass (k, j)
+                    const int i = ((t / j) * 2 * j) + (t % j);
+                    const float a = v[i], c = v[i + j];
+                    const bool up = (i & k) == 0;
+                    if ((a > c) == up) {
+                        v[i] = c;
+                        v[i + j] = a;
+                    }
+                }
+                __syncthreads();
+            }
+        }
+        const float last_index = (float)(n - 1);
+        for (int e = lane; e < n_entries; e += 64) {
+            // each product and difference rounded on its own, as torch's
+            // CPU quantile computes them: no contraction into fma here
+#pragma clang fp contract(off)
+            const float rank = qf.q[e] * last_index;
+            const int lo = (int)rank;
+            const int hi = (int)ceilf(rank);
+            const float wt = rank - (float)lo;
+            const float a = v[lo], c = v[hi];
+            const float r = fabsf(wt) < 0.5f ? __builtin_fmaf(wt, c - a, a)
+                                             : __builtin_fmaf(wt - 1.0f, c - a, c);
+            cb[b * n_entries + e] = r;
+        }
+        __syncthreads();
+    }
+}
+
 template <bool kBF16>
 __global__ __launch_bounds__(kThreads) void dequant_kernel(
     const uint8_t* __restrict__ packed, int64_t nbytes,
@@ -199,6 +263,19 @@ int launch_quantize_pack(const float* w, int64_t total, const float* codebook,
             }
     }
     return check_launch("nb_quantize_pack");
+}
+
+int launch_block_codebooks(const float* w, int64_t total, int64_t num_blocks, int block_size,
+                           int n_entries, const float* q, float* cb, hipStream_t stream) {
+    if (num_blocks == 0) return NB_OK;
+    QuantileFractions qf;
+    for (int e = 0; e < kCbMaxEntries; ++e) qf.q[e] = e < n_entries ? q[e] : 0.f;
+    int64_t grid = num_blocks;
+    const int64_t cap = (int64_t)device_cu_count() * 32;
+    if (grid > cap) grid = cap;
+    hipLaunchKernelGGL(block_codebooks_kernel, dim3((int)grid), dim3(64), 0, stream, w, total,
+                       num_blocks, block_size, n_entries, qf, cb);
+    return check_launch("nb_block_codebooks");
 }
 
 int launch_dequant(const uint8_t* packed, const float* codebook, void* w,

@@ -102,6 +102,8 @@ int launch_unpack(const uint8_t* packed, uint8_t* out, int64_t count, int bits,
                   hipStream_t stream);
 int launch_pack(const uint8_t* idx, uint8_t* out, int64_t count, int bits,
                 hipStream_t stream);
+int launch_block_codebooks(const float* w, int64_t total, int64_t num_blocks, int block_size,
+                           int n_entries, const float* q, float* cb, hipStream_t stream);
 int launch_quantize_pack(const float* w, int64_t total, const float* codebook,
                          int64_t num_blocks, int n_entries, int block_size, int bits,
                          uint8_t* out, hipStream_t stream);

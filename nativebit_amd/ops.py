@@ -91,6 +91,22 @@ def gemv(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
     return out.reshape(N) if squeeze else out
 
 
+def block_codebooks(w: torch.Tensor, n_entries: int, block_size: int) -> torch.Tensor:
+    """Per-block quantile codebooks of the flat weights ``w``:
+    (ceil(total / block_size), n_entries) fp32, torch.quantile(w_block,
+    linspace(0, 1, n_entries)) per block (nativebit/codebook_utils.py:6-22,
+    nativebit/layers.py:76), the last block over the weights that exist."""
+    _require_cuda("w", w)
+    if w.dtype != torch.float32:
+        raise TypeError("w must be float32")
+    w = w.contiguous().reshape(-1)
+    nb = -(-w.numel() // block_size)
+    out = torch.empty(nb, n_entries, dtype=torch.float32, device=w.device)
+    _lib.check(_lib.load().nb_block_codebooks(w.data_ptr(), w.numel(), block_size, n_entries,
+                                              out.data_ptr(), _stream(w)))
+    return out
+
+
 def quantize_pack(w: torch.Tensor, codebook: torch.Tensor, block_size: int,
                   bits: int | None = None) -> torch.Tensor:
     """Nearest-entry indices of the flat weights ``w`` against per-block

@@ -190,6 +190,31 @@ def test_batch_fused_forms_validation():
     assert batched(_lib.NB_BF16, *base, 0, Y, None, 0.0, 0) == _lib.NB_EUNSUPPORTED
 
 
+def test_linspace01_equals_torch():
+    """The quantile fractions of nb_block_codebooks are torch.linspace's,
+    bit for bit, for every entry count it takes."""
+    import torch
+    lib = _lib.load()
+    for n in range(1, 257):
+        buf = (ctypes.c_float * n)()
+        assert lib.nb_linspace01(n, buf) == _lib.NB_OK
+        assert torch.equal(torch.tensor(list(buf), dtype=torch.float32), torch.linspace(0, 1, n)), n
+    assert lib.nb_linspace01(0, (ctypes.c_float * 1)()) == _lib.NB_EINVAL
+    assert lib.nb_linspace01(257, (ctypes.c_float * 257)()) == _lib.NB_EINVAL
+
+
+def test_block_codebooks_validation():
+    c = _lib.load().nb_block_codebooks
+    assert c(FAKE, 0, 128, 8, FAKE, None) == _lib.NB_OK
+    assert c(FAKE, 100, 0, 8, FAKE, None) == _lib.NB_EUNSUPPORTED
+    assert c(FAKE, 100, 1025, 8, FAKE, None) == _lib.NB_EUNSUPPORTED
+    assert c(FAKE, 100, 128, 0, FAKE, None) == _lib.NB_EUNSUPPORTED
+    assert c(FAKE, 100, 128, 257, FAKE, None) == _lib.NB_EUNSUPPORTED
+    assert c(FAKE, -1, 128, 8, FAKE, None) == _lib.NB_EINVAL
+    assert c(None, 100, 128, 8, FAKE, None) == _lib.NB_EINVAL
+    assert c(FAKE + 2, 100, 128, 8, FAKE, None) == _lib.NB_EALIGN
+
+
 def test_quantize_pack_validation():
     """nb_quantize_pack: format and tiling checks on the host."""
     q = _lib.load().nb_quantize_pack

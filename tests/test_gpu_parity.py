@@ -109,6 +109,25 @@ def test_quantize_pack_bit_exact(dev, total, ne, bs, bits):
     assert np.array_equal(got.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("total,ne,bs", [
+    (6912 * 2560, 8, 128), (1000, 8, 128), (777, 4, 64), (4096 + 17, 16, 256), (3000, 8, 1000),
+    (55, 3, 5), (300, 1, 128), (1024, 256, 128), (2, 8, 128), (640, 2, 1024),
+])
+def test_block_codebooks_equal_torch_quantile(dev, total, ne, bs):
+    """GPU per-block quantile codebooks equal torch.quantile on the CPU over
+    the same blocks (the reference's init_codebook_percentile per block,
+    codebook_utils.py:6-22, layers.py:76), bit for bit, tail block over the
+    weights that exist; repeated values included."""
+    note(f"block_codebooks total={total} ne={ne} bs={bs}")
+    g = torch.Generator().manual_seed(total + ne)
+    w = torch.randn(total, generator=g) * 0.02
+    w[::7] = w[total // 2]                           # repeated values
+    ref = synth.block_codebooks(w, total, ne, bs)
+    got = ops.block_codebooks(w.to(dev), ne, bs).cpu()
+    assert got.shape == ref.shape
+    assert torch.equal(got, ref), int((got != ref).sum())
+
+
 def test_quantize_pack_roundtrip_synth(dev):
     """The synthetic generator's torch quantization (squared distance argmin,
     per-block quantile codebooks) packed by nb_pack equals nb_quantize_pack
