@@ -84,7 +84,7 @@ def parse():
                    help="CPU baseline passes continue until this much time has been spent")
     p.add_argument("--no-extra", action="store_true",
                    help="skip the decode / prefill / skinny / sweep configurations")
-    p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep,quantize",
+    p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep,quantize,codec",
                    help="comma list of extra configurations to run")
     p.add_argument("--random-weights", action="store_true",
                    help="uniformly random index bytes and codebooks instead of quantized "
@@ -460,6 +460,50 @@ def bench_codebooks(w, total):
                 ops.block_codebooks(w, NE, BS), synth.block_codebooks(w, total, NE, BS)))}
 
 
+def bench_codec(dev):
+    """The format kernels on one 6912x2560 layer at 2, 3 and 4 bits: nb_unpack
+    (stream -> uint8 indices), nb_pack (indices -> stream; the reference's
+    pack_nbits is a per-bit Python loop, nativebit/pack.py:97-138) and
+    nb_dequant to fp32 / bf16 (the reference's gather, pack.py:145-169).
+    Bytes = what each kernel must read and write; every timed launch of a
+    graph reads a different copy (copies x bytes > 512 MB)."""
+    from nativebit_amd import ops
+    N, K = 6912, 2560
+    total = N * K
+    out = {}
+    gen = torch.Generator(device=dev).manual_seed(13)
+    for bits in (2, 3, 4):
+        ne = 1 << bits
+        pb = ops.packed_nbytes(total, bits)
+        nb = total // BS
+        copies = max(2, -(-(512 << 20) // (total + pb)))
+        idx = [torch.randint(0, ne, (total,), dtype=torch.uint8, device=dev, generator=gen)
+               for _ in range(copies)]
+        ps = [ops.pack(i, bits) for i in idx]
+        cbs = [torch.randn(nb, ne, device=dev, generator=gen) for _ in range(copies)]
+        res = {}
+        for name, fn, nbytes in (
+                ("unpack", lambda i: ops.unpack(ps[i], total, bits), pb + total),
+                ("pack", lambda i: ops.pack(idx[i], bits), total + pb),
+                ("dequant_f32", lambda i: ops.dequant(ps[i], cbs[i], total, bits, BS),
+                 pb + nb * ne * 4 + total * 4),
+                ("dequant_bf16", lambda i: ops.dequant(ps[i], cbs[i], total, bits, BS,
+                                                       torch.bfloat16),
+                 pb + nb * ne * 4 + total * 2)):
+            def run():
+                for i in range(copies):
+                    fn(i)
+            ms = graph_time(run, 10, 3) / copies
+            res[name] = {"us": round(ms * 1e3, 2), "GB_s": round(nbytes / ms / 1e6, 1),
+                         "pct_hbm_peak": round(nbytes / ms / 1e6 / HBM_PEAK_GBS * 100, 1),
+                         "bytes": nbytes}
+        out[f"bits{bits}"] = res
+        del idx, ps, cbs
+    out["note"] = ("6912x2560 weights, block 128, one launch per copy inside a HIP graph; "
+                   "unpack and pack verified against the oracle in tests/test_gpu_parity.py")
+    return out
+
+
 def bench_sweep(dev):
     """Config 3: bit width x block size at batch 1 (nb_gemv)."""
     from nativebit_amd import ops, synth
@@ -602,7 +646,8 @@ def main():
                          ("prefill", lambda: bench_prefill(dev, args.random_weights)),
                          ("skinny", lambda: bench_skinny(dev, layers)),
                          ("sweep", lambda: bench_sweep(dev)),
-                         ("quantize", lambda: bench_quantize(dev))):
+                         ("quantize", lambda: bench_quantize(dev)),
+                         ("codec", lambda: bench_codec(dev))):
             if name not in wanted_extra:
                 continue
             t0 = time.time()

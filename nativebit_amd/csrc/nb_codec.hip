@@ -1,14 +1,19 @@
 // Bit-exact format kernels: unpack, pack and dequantize NativeBit index
-// streams on gfx950.  These are the parity kernels of the path (their
-// outputs must equal the reference's byte for byte), not the hot loop, so
-// they favour simple, obviously-correct indexing over peak bandwidth; all of
-// them are coalesced grid-stride loops.
+// streams on gfx950 (their outputs must equal the reference's byte for
+// byte).  The bulk of a stream goes through chunk kernels: a chunk is 32
+// indices = 4 groups of 8 = BITS whole dwords of the LSB-first stream, so a
+// thread moves BITS dwords one way and 32 index bytes (or 32 weights) the
+// other with wide loads and stores, its field offsets fixed at compile time.
+// The last count % 32 indices, and pointers without the chunk kernels'
+// alignment, go through per-element grid-stride kernels.
 //
 // Reference semantics: nativebit/pack.py:21-169 (pack_3bit, unpack_3bit,
 // pack_4bit, unpack_4bit, pack_nbits, unpack_nbits, reconstruct_weight),
 // inference/triton_kernel.py:199-220 (pack_indices_to_3bit),
 // inference/pack.py:21-35 (quantize_weight, fused here with the pack).
 #include <math.h>
+
+#include <type_traits>
 
 #include "nb_device.h"
 #include "nb_internal.h"
@@ -29,9 +34,9 @@ inline int grid_for(int64_t n) {
 
 __global__ __launch_bounds__(kThreads) void unpack_kernel(
     const uint8_t* __restrict__ packed, int64_t nbytes,
-    uint8_t* __restrict__ out, int64_t count, int bits) {
+    uint8_t* __restrict__ out, int64_t first, int64_t count, int bits) {
     const int64_t stride = (int64_t)gridDim.x * kThreads;
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
+    for (int64_t i = first + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < count;
          i += stride) {
         out[i] = (uint8_t)read_field(packed, nbytes, i, bits);
     }
@@ -41,10 +46,10 @@ __global__ __launch_bounds__(kThreads) void unpack_kernel(
 // the fields of indices floor(8b/bits) .. floor((8b+7)/bits).
 __global__ __launch_bounds__(kThreads) void pack_kernel(
     const uint8_t* __restrict__ idx, int64_t count, int bits,
-    uint8_t* __restrict__ out, int64_t nbytes) {
+    uint8_t* __restrict__ out, int64_t first_byte, int64_t nbytes) {
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     const uint32_t mask = (1u << bits) - 1u;
-    for (int64_t b = (int64_t)blockIdx.x * kThreads + threadIdx.x; b < nbytes;
+    for (int64_t b = first_byte + (int64_t)blockIdx.x * kThreads + threadIdx.x; b < nbytes;
          b += stride) {
         const int64_t first_bit = b * 8;
         const int64_t i0 = first_bit / bits;
@@ -203,11 +208,11 @@ __global__ __launch_bounds__(64) void block_codebooks_kernel(
 template <bool kBF16>
 __global__ __launch_bounds__(kThreads) void dequant_kernel(
     const uint8_t* __restrict__ packed, int64_t nbytes,
-    const float* __restrict__ cb, void* __restrict__ w, int64_t total,
+    const float* __restrict__ cb, void* __restrict__ w, int64_t first, int64_t total,
     int bits, int n_entries, int block_size) {
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     const uint32_t last = (uint32_t)(n_entries - 1);
-    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+    for (int64_t i = first + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
          i += stride) {
         uint32_t e = read_field(packed, nbytes, i, bits);
         e = e < last ? e : last;
@@ -220,14 +225,192 @@ __global__ __launch_bounds__(kThreads) void dequant_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// chunk kernels (32 indices <-> BITS dwords)
+// ---------------------------------------------------------------------------
+// Field j (0..31) of a chunk: bits [j*BITS, (j+1)*BITS) of the little-endian
+// dwords d; j is a constant once the callers' loops are unrolled.
+template <int BITS>
+__device__ __forceinline__ uint32_t chunk_field(const uint32_t (&d)[BITS], int j) {
+    const int bit = j * BITS;
+    const int w = bit >> 5;
+    const int off = bit & 31;
+    const uint32_t mask = (1u << BITS) - 1u;
+    if (off + BITS > 32) return __builtin_amdgcn_alignbit(d[w + 1], d[w], off) & mask;
+    return (d[w] >> off) & mask;
+}
+
+template <int BITS>
+__device__ __forceinline__ void load_chunk(const uint32_t* __restrict__ packed, int64_t c,
+                                           uint32_t (&d)[BITS]) {
+    const uint32_t* p = packed + c * BITS;
+#pragma unroll
+    for (int w = 0; w < BITS; ++w) d[w] = __builtin_nontemporal_load(p + w);
+}
+
+// Stores the Q 16-byte pieces of each lane's chunk so that every store
+// instruction of the wave writes 64 consecutive pieces (1 KiB): the pieces go
+// through the wave's LDS area (lane pitch Q + 1 pieces) and come back in
+// output order.  Lane l holds chunk c0 + l; pieces at or past `limit` (the
+// end of the output, counted from dst) are not stored.  Every lane of the
+// wave calls this.  A wave's LDS operations complete in issue order, so the
+// fences only keep the compiler from moving the accesses.
+template <int Q>
+__device__ __forceinline__ void wave_store_pieces(uint4* __restrict__ lds, const uint4 (&v)[Q],
+                                                  uint4* __restrict__ dst, int64_t c0,
+                                                  int64_t limit, int lane) {
+#pragma unroll
+    for (int q = 0; q < Q; ++q) lds[lane * (Q + 1) + q] = v[q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int k = 0; k < Q; ++k) {
+        const int i = k * 64 + lane;  // piece of the wave's output
+        const uint4 u = lds[(i / Q) * (Q + 1) + (i % Q)];
+        const int64_t o = c0 * Q + i;
+        if (o < limit) dst[o] = u;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Grid-stride over chunks in whole waves: the loop condition is the wave's
+// first chunk, so every lane of a wave runs the same iterations (the wave
+// store needs all of them); lanes past the last chunk compute on chunk 0
+// and store nothing.
+#define NB_CHUNK_LOOP(chunks)                                                        \
+    const int lane = threadIdx.x & 63;                                               \
+    const int64_t stride = (int64_t)gridDim.x * kThreads;                            \
+    for (int64_t c0 = (int64_t)blockIdx.x * kThreads + (threadIdx.x & ~63); c0 < (chunks); \
+         c0 += stride)
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void unpack_chunks_kernel(
+    const uint32_t* __restrict__ packed, uint4* __restrict__ out, int64_t chunks) {
+    __shared__ uint4 lds[kThreads / 64][64 * 3];
+    NB_CHUNK_LOOP(chunks) {
+        const int64_t c = c0 + lane < chunks ? c0 + lane : 0;
+        uint32_t d[BITS];
+        load_chunk<BITS>(packed, c, d);
+        uint32_t o[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            o[k] = chunk_field<BITS>(d, 4 * k) | (chunk_field<BITS>(d, 4 * k + 1) << 8) |
+                   (chunk_field<BITS>(d, 4 * k + 2) << 16) | (chunk_field<BITS>(d, 4 * k + 3) << 24);
+        }
+        const uint4 v[2] = {make_uint4(o[0], o[1], o[2], o[3]), make_uint4(o[4], o[5], o[6], o[7])};
+        wave_store_pieces<2>(lds[threadIdx.x >> 6], v, out, c0, 2 * chunks, lane);
+    }
+}
+
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void pack_chunks_kernel(
+    const uint4* __restrict__ idx, uint32_t* __restrict__ out, int64_t chunks) {
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    const uint32_t mask = (1u << BITS) - 1u;
+    for (int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x; c < chunks; c += stride) {
+        const uint4 a = idx[2 * c], b = idx[2 * c + 1];
+        const uint32_t in[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint32_t o[BITS];
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) o[w] = 0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const uint32_t f = (in[j >> 2] >> (8 * (j & 3))) & mask;
+            const int bit = j * BITS;
+            const int w = bit >> 5;
+            const int off = bit & 31;
+            o[w] |= f << off;
+            if (off + BITS > 32) o[w + 1] |= f >> (32 - off);
+        }
+        uint32_t* p = out + c * BITS;
+#pragma unroll
+        for (int w = 0; w < BITS; ++w) p[w] = o[w];
+    }
+}
+
+// block_size % 32 == 0, so a chunk lies inside one block.
+template <int BITS, bool kBF16>
+__global__ __launch_bounds__(kThreads) void dequant_chunks_kernel(
+    const uint32_t* __restrict__ packed, const float* __restrict__ cb, void* __restrict__ w,
+    int64_t chunks, int n_entries, int block_size) {
+    constexpr int Q = kBF16 ? 4 : 8;  // 16-byte pieces per chunk
+    __shared__ uint4 lds[kThreads / 64][64 * (Q + 1)];
+    const uint32_t last = (uint32_t)(n_entries - 1);
+    NB_CHUNK_LOOP(chunks) {
+        const int64_t c = c0 + lane < chunks ? c0 + lane : 0;
+        uint32_t d[BITS];
+        load_chunk<BITS>(packed, c, d);
+        const float* tab = cb + (c * 32 / block_size) * n_entries;
+        float v[32];
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const uint32_t e = chunk_field<BITS>(d, j);
+            v[j] = tab[e < last ? e : last];
+        }
+        uint4 pc[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            if (kBF16) {
+                uint32_t h[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    h[k] = (uint32_t)f32_to_bf16_rne(v[8 * q + 2 * k]) |
+                           ((uint32_t)f32_to_bf16_rne(v[8 * q + 2 * k + 1]) << 16);
+                }
+                pc[q] = make_uint4(h[0], h[1], h[2], h[3]);
+            } else {
+                pc[q] = make_uint4(__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]),
+                                   __float_as_uint(v[4 * q + 2]), __float_as_uint(v[4 * q + 3]));
+            }
+        }
+        wave_store_pieces<Q>(lds[threadIdx.x >> 6], pc, static_cast<uint4*>(w), c0, Q * chunks,
+                             lane);
+    }
+}
+
+// f(std::integral_constant<int, bits>) for bits 1..8.
+template <typename F>
+void with_bits(int bits, F&& f) {
+    switch (bits) {
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        case 3: f(std::integral_constant<int, 3>{}); break;
+        case 4: f(std::integral_constant<int, 4>{}); break;
+        case 5: f(std::integral_constant<int, 5>{}); break;
+        case 6: f(std::integral_constant<int, 6>{}); break;
+        case 7: f(std::integral_constant<int, 7>{}); break;
+        case 8: f(std::integral_constant<int, 8>{}); break;
+    }
+}
+
+inline bool is_aligned(const void* p, uintptr_t a) { return reinterpret_cast<uintptr_t>(p) % a == 0; }
+
 }  // namespace
 
 int launch_unpack(const uint8_t* packed, uint8_t* out, int64_t count, int bits,
                   hipStream_t stream) {
     if (count == 0) return NB_OK;
-    hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(count)), dim3(kThreads), 0,
-                       stream, packed, packed_nbytes(count, bits), out, count,
-                       bits);
+    const int64_t nbytes = packed_nbytes(count, bits);
+    int64_t first = 0;
+    if (is_aligned(packed, 4) && is_aligned(out, 16)) {
+        const int64_t chunks = count / 32;
+        if (chunks > 0) {
+            with_bits(bits, [&](auto B) {
+                hipLaunchKernelGGL(unpack_chunks_kernel<decltype(B)::value>, dim3(grid_for(chunks)),
+                                   dim3(kThreads), 0, stream,
+                                   reinterpret_cast<const uint32_t*>(packed),
+                                   reinterpret_cast<uint4*>(out), chunks);
+            });
+            first = chunks * 32;
+        }
+    }
+    if (first < count) {
+        hipLaunchKernelGGL(unpack_kernel, dim3(grid_for(count - first)), dim3(kThreads), 0,
+                           stream, packed, nbytes, out, first, count, bits);
+    }
     return check_launch("nb_unpack");
 }
 
@@ -235,8 +418,26 @@ int launch_pack(const uint8_t* idx, uint8_t* out, int64_t count, int bits,
                 hipStream_t stream) {
     const int64_t nbytes = packed_nbytes(count, bits);
     if (nbytes == 0) return NB_OK;
-    hipLaunchKernelGGL(pack_kernel, dim3(grid_for(nbytes)), dim3(kThreads), 0,
-                       stream, idx, count, bits, out, nbytes);
+    // chunk c writes stream bytes [4 * bits * c, 4 * bits * (c + 1)) from
+    // indices [32c, 32c + 32); the per-byte kernel writes the rest, padding
+    // included
+    int64_t first_byte = 0;
+    if (is_aligned(idx, 16) && is_aligned(out, 4)) {
+        const int64_t chunks = count / 32;
+        if (chunks > 0) {
+            with_bits(bits, [&](auto B) {
+                hipLaunchKernelGGL(pack_chunks_kernel<decltype(B)::value>, dim3(grid_for(chunks)),
+                                   dim3(kThreads), 0, stream,
+                                   reinterpret_cast<const uint4*>(idx),
+                                   reinterpret_cast<uint32_t*>(out), chunks);
+            });
+            first_byte = chunks * 4 * bits;
+        }
+    }
+    if (first_byte < nbytes) {
+        hipLaunchKernelGGL(pack_kernel, dim3(grid_for(nbytes - first_byte)), dim3(kThreads), 0,
+                           stream, idx, count, bits, out, first_byte, nbytes);
+    }
     return check_launch("nb_pack");
 }
 
@@ -284,16 +485,28 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
     if (total == 0) return NB_OK;
     (void)num_blocks;  // validated by the caller: num_blocks * block_size >= total
     // Fields of indices < total lie inside the first packed_nbytes(total)
-    // bytes, so that is all the kernel may touch.
+    // bytes, so that is all the kernels may touch.
     const int64_t nbytes = packed_nbytes(total, bits);
-    if (w_dtype == NB_BF16) {
-        hipLaunchKernelGGL(dequant_kernel<true>, dim3(grid_for(total)),
-                           dim3(kThreads), 0, stream, packed, nbytes, codebook,
-                           w, total, bits, n_entries, block_size);
-    } else {
-        hipLaunchKernelGGL(dequant_kernel<false>, dim3(grid_for(total)),
-                           dim3(kThreads), 0, stream, packed, nbytes, codebook,
-                           w, total, bits, n_entries, block_size);
+    const bool bf16 = w_dtype == NB_BF16;
+    int64_t first = 0;
+    if (block_size % 32 == 0 && is_aligned(packed, 4) && is_aligned(w, 16)) {
+        const int64_t chunks = total / 32;
+        if (chunks > 0) {
+            with_bits(bits, [&](auto B) {
+                constexpr int kB = decltype(B)::value;
+                auto kernel = bf16 ? dequant_chunks_kernel<kB, true> : dequant_chunks_kernel<kB, false>;
+                hipLaunchKernelGGL(kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream,
+                                   reinterpret_cast<const uint32_t*>(packed), codebook, w, chunks,
+                                   n_entries, block_size);
+            });
+            first = chunks * 32;
+        }
+    }
+    if (first < total) {
+        auto kernel = bf16 ? dequant_kernel<true> : dequant_kernel<false>;
+        hipLaunchKernelGGL(kernel, dim3(grid_for(total - first)), dim3(kThreads), 0, stream,
+                           packed, nbytes, codebook, w, first, total, bits, n_entries,
+                           block_size);
     }
     return check_launch("nb_dequant");
 }

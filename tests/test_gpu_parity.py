@@ -67,9 +67,32 @@ def test_golden_streams_on_gpu(dev, golden):
         assert ops.unpack(p, len(v["indices"]), v["bits"]).tolist() == v["indices"]
 
 
+@pytest.mark.parametrize("bits", [1, 3, 5, 8])
+def test_codec_unaligned_pointers(dev, bits):
+    """Streams and index arrays that start at an odd byte address (the
+    per-element kernels) give the same bytes as aligned ones (the chunk
+    kernels), tails included."""
+    n = 32 * 37 + 11
+    note(f"unaligned codec bits={bits} n={n}")
+    rng = np.random.default_rng(bits)
+    idx = rng.integers(0, 1 << bits, n, dtype=np.uint8)
+    ref = O.pack(idx, bits)
+    buf = torch.zeros(n + 1, dtype=torch.uint8, device=dev)
+    buf[1:] = torch.from_numpy(idx).to(dev)
+    assert np.array_equal(ops.pack(buf[1:], bits).cpu().numpy(), ref)
+    sbuf = torch.zeros(ref.size + 1, dtype=torch.uint8, device=dev)
+    sbuf[1:] = torch.from_numpy(ref).to(dev)
+    assert np.array_equal(ops.unpack(sbuf[1:], n, bits).cpu().numpy(), idx)
+    ne = 1 << bits
+    cb = rng.standard_normal((-(-n // 64), ne)).astype(np.float32)
+    w = ops.dequant(sbuf[1:], torch.from_numpy(cb).to(dev), n, bits, 64)
+    assert np.array_equal(w.cpu().numpy(), O.dequant(idx, cb, 64, n))
+
+
 @pytest.mark.parametrize("N,K,bits,ne,bs", [
     (6912, 2560, 3, 8, 128), (2560, 6912, 3, 8, 128), (100, 37, 3, 8, 128),
     (64, 512, 2, 4, 64), (64, 512, 4, 16, 256), (33, 65, 5, 20, 16), (17, 9, 3, 5, 8),
+    (48, 640, 5, 20, 64), (40, 96, 8, 200, 32), (3, 100, 1, 2, 32), (7, 160, 6, 64, 96),
 ])
 def test_dequant_bit_exact(dev, N, K, bits, ne, bs):
     note(f"dequant N={N} K={K} bits={bits} ne={ne} bs={bs}")
