@@ -206,7 +206,7 @@ __device__ __forceinline__ float slice_dot(const uint32_t (&d)[BITS], uint32_t b
 // Pipeline depth of the streaming kernel (row-sets whose loads are in flight
 // per lane) and resident workgroups per CU it is launched with.
 #ifndef NB_GEMV_DEPTH
-#define NB_GEMV_DEPTH 4
+#define NB_GEMV_DEPTH 2
 #endif
 #ifndef NB_GEMV_WG_PER_CU
 #define NB_GEMV_WG_PER_CU 4
@@ -234,8 +234,7 @@ __device__ __forceinline__ void issue_set(const uint32_t* __restrict__ packed,
 // Each workgroup streams a contiguous range of row-sets.  Lane registers
 // hold a ring of D row-sets: the loads of set i+D are issued right after set
 // i has been consumed, so every lane keeps D sets of HBM requests in flight
-// while it computes.  The weight loads of the first D sets are issued before
-// the activations are fetched, so the two latencies overlap.
+// while it computes.
 template <int BITS, int BS, bool kXBF16, int D>
 __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ packed,
@@ -272,6 +271,11 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
         const int r = (set < last_set ? set : last_set) * P + row_sub;
         return r < N ? r : N - 1;
     };
+    // The activations are requested first: a wave's loads retire in issue
+    // order, so set 0 can be computed as soon as it and x are in while the
+    // later sets are still arriving.
+    float xr[32];
+    load_x_slice<kXBF16>(x, s, xr);
     uint32_t d[D][BITS];
     float cv[D][EPL];
 #pragma unroll
@@ -279,9 +283,6 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(
         issue_set<BITS, BS, EPL>(packed, cb, clamp_row(set_begin + st), S, s, bpr, q,
                                  d[st], cv[st]);
     }
-
-    float xr[32];
-    load_x_slice<kXBF16>(x, s, xr);
 
     for (int base = 0; base < count; base += D) {
 #pragma unroll
