@@ -70,9 +70,9 @@ __global__ __launch_bounds__(kThreads) void pack_kernel(
 // (the padded tail of the last block) are 0.0.  Inputs are finite.
 __device__ __forceinline__ uint32_t nearest_entry(const float* __restrict__ w, int64_t total,
                                                   const float* __restrict__ cb, int n_entries,
-                                                  int block_size, int64_t i) {
+                                                  int64_t blk, int64_t i) {
     const float v = i < total ? w[i] : 0.f;
-    const float* c = cb + (i / block_size) * n_entries;
+    const float* c = cb + blk * n_entries;
     float d = v - c[0];
     float best_d = d * d;
     uint32_t best = 0;
@@ -97,21 +97,30 @@ __device__ __forceinline__ uint32_t nearest_entry(const float* __restrict__ w, i
 template <bool kSmallNE, int NE>
 __global__ __launch_bounds__(kThreads) void quantize_pack_kernel(
     const float* __restrict__ w, int64_t total, const float* __restrict__ cb, int n_entries,
-    int block_size, int64_t count, int bits, uint8_t* __restrict__ out, int64_t nbytes) {
+    int block_size, int64_t count, int bits, uint8_t* __restrict__ out, int64_t nbytes,
+    int64_t first_group) {
     const int64_t stride = (int64_t)gridDim.x * kThreads;
     const int64_t groups = (count + 7) / 8;
-    for (int64_t t = (int64_t)blockIdx.x * kThreads + threadIdx.x; t < groups; t += stride) {
+    for (int64_t t = first_group + (int64_t)blockIdx.x * kThreads + threadIdx.x; t < groups;
+         t += stride) {
         float c[16];
         int64_t cur_block = -1;
         uint64_t acc = 0;  // 8 fields, LSB first (8 * bits <= 64)
+        // block of index 8t + j, advanced one index at a time (one division
+        // per group, not per weight)
+        int64_t blk = (8 * t) / block_size;
+        int in_blk = (int)(8 * t - blk * block_size);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const int64_t i = 8 * t + j;
+            if (j > 0 && ++in_blk == block_size) {
+                in_blk = 0;
+                ++blk;
+            }
             uint32_t f = 0;
             if (i < count) {
                 if (kSmallNE) {
                     const float v = i < total ? w[i] : 0.f;
-                    const int64_t blk = i / block_size;
                     constexpr int kE = NE ? NE : 16;
                     if (blk != cur_block) {
                         cur_block = blk;
@@ -130,7 +139,7 @@ __global__ __launch_bounds__(kThreads) void quantize_pack_kernel(
                         }
                     }
                 } else {
-                    f = nearest_entry(w, total, cb, n_entries, block_size, i);
+                    f = nearest_entry(w, total, cb, n_entries, blk, i);
                 }
             }
             acc |= (uint64_t)f << (j * bits);
@@ -140,6 +149,63 @@ __global__ __launch_bounds__(kThreads) void quantize_pack_kernel(
             const int64_t ob = (int64_t)bits * t + k;
             if (ob < nbytes) out[ob] = (uint8_t)(acc >> (8 * k));
         }
+    }
+}
+
+// Quantize-at-pack for the standard formats (NE = 2^BITS entries, blocks a
+// multiple of 32 weights): one thread per chunk of 32 real weights, which
+// lies in one block -- the block's NE entries and the 32 weights come in
+// with vector loads, the nearest-entry search is the same squared-distance
+// compare (first index on ties), and the 32 fields leave as BITS dwords.
+template <int BITS>
+__global__ __launch_bounds__(kThreads) void quantize_chunks_kernel(
+    const float4* __restrict__ w, const float4* __restrict__ cb, int block_size,
+    uint32_t* __restrict__ out, int64_t chunks) {
+    constexpr int NE = 1 << BITS;
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t c = (int64_t)blockIdx.x * kThreads + threadIdx.x; c < chunks; c += stride) {
+        const float4* tp = cb + (c * 32 / block_size) * (NE / 4);
+        float t[NE];
+#pragma unroll
+        for (int q = 0; q < NE / 4; ++q) {
+            const float4 u = tp[q];
+            t[4 * q] = u.x;
+            t[4 * q + 1] = u.y;
+            t[4 * q + 2] = u.z;
+            t[4 * q + 3] = u.w;
+        }
+        float v[32];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const float4 u = w[8 * c + q];
+            v[4 * q] = u.x;
+            v[4 * q + 1] = u.y;
+            v[4 * q + 2] = u.z;
+            v[4 * q + 3] = u.w;
+        }
+        uint32_t o[BITS];
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) o[k] = 0;
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            float d = v[j] - t[0];
+            float best_d = d * d;
+            uint32_t f = 0;
+#pragma unroll
+            for (int e = 1; e < NE; ++e) {
+                d = v[j] - t[e];
+                const float dd = d * d;
+                if (dd < best_d) {
+                    best_d = dd;
+                    f = (uint32_t)e;
+                }
+            }
+            const int bit = j * BITS;
+            o[bit >> 5] |= f << (bit & 31);
+            if ((bit & 31) + BITS > 32) o[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
+        }
+#pragma unroll
+        for (int k = 0; k < BITS; ++k) out[c * BITS + k] = o[k];
     }
 }
 
@@ -447,10 +513,32 @@ int launch_quantize_pack(const float* w, int64_t total, const float* codebook,
     const int64_t count = num_blocks * block_size;
     const int64_t nbytes = packed_nbytes(count, bits);
     if (nbytes == 0) return NB_OK;
-    const int grid = grid_for((count + 7) / 8);
+    // chunks of 32 real weights in the standard formats; the general kernel
+    // takes the remaining groups (the tail and the zero-padded weights)
+    int64_t first_group = 0;
+    if ((n_entries == 4 || n_entries == 8 || n_entries == 16) && n_entries == (1 << bits) &&
+        block_size % 32 == 0 && is_aligned(w, 16) && is_aligned(codebook, 16) &&
+        is_aligned(out, 4)) {
+        const int64_t chunks = total / 32;
+        if (chunks > 0) {
+            auto chunk = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, dim3(grid_for(chunks)), dim3(kThreads), 0, stream,
+                                   reinterpret_cast<const float4*>(w),
+                                   reinterpret_cast<const float4*>(codebook), block_size,
+                                   reinterpret_cast<uint32_t*>(out), chunks);
+            };
+            if (bits == 2) chunk(quantize_chunks_kernel<2>);
+            if (bits == 3) chunk(quantize_chunks_kernel<3>);
+            if (bits == 4) chunk(quantize_chunks_kernel<4>);
+            first_group = chunks * 4;
+        }
+    }
+    const int64_t groups = (count + 7) / 8;
+    if (first_group >= groups) return check_launch("nb_quantize_pack");
+    const int grid = grid_for(groups - first_group);
     auto go = [&](auto kernel) {
         hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, w, total, codebook,
-                           n_entries, block_size, count, bits, out, nbytes);
+                           n_entries, block_size, count, bits, out, nbytes, first_group);
     };
     switch (n_entries) {
         case 4: go(quantize_pack_kernel<true, 4>); break;
