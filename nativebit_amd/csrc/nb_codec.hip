@@ -271,6 +271,79 @@ __global__ __launch_bounds__(64) void block_codebooks_kernel(
     }
 }
 
+// The same codebooks for blocks of at most 64 * H weights, sorted in one
+// wave's registers: value i of the (+inf padded) block sits in lane i % 64,
+// slot i / 64; each bitonic pass pairs i with i ^ j (a cross-lane shuffle for
+// j < 64, another slot of the same lane otherwise) and keeps the min or the
+// max, so no LDS and no barrier is involved.  Entries are then formed as in
+// block_codebooks_kernel from values fetched by shuffles.
+template <int H>
+__device__ __forceinline__ float sorted_at(const float (&v)[H], int idx) {
+    float r = __shfl(v[0], idx & 63, 64);
+#pragma unroll
+    for (int h = 1; h < H; ++h) {
+        const float u = __shfl(v[h], idx & 63, 64);
+        r = (idx >> 6) == h ? u : r;
+    }
+    return r;
+}
+
+template <int H>
+__global__ __launch_bounds__(kThreads) void block_codebooks_wave_kernel(
+    const float* __restrict__ w, int64_t total, int64_t num_blocks, int block_size, int n_entries,
+    QuantileFractions qf, float* __restrict__ cb) {
+    constexpr int P = 64 * H;
+    const int lane = threadIdx.x & 63;
+    const int64_t nwaves = ((int64_t)gridDim.x * kThreads) >> 6;
+    for (int64_t b = ((int64_t)blockIdx.x * kThreads + threadIdx.x) >> 6; b < num_blocks;
+         b += nwaves) {
+        const int64_t first = b * block_size;
+        const int n = (int)min((int64_t)block_size, total - first);
+        float v[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const int i = lane + 64 * h;
+            v[h] = i < n ? w[first + i] : INFINITY;
+        }
+#pragma unroll
+        for (int k = 2; k <= P; k <<= 1) {
+#pragma unroll
+            for (int j = k >> 1; j > 0; j >>= 1) {
+                float o[H];
+#pragma unroll
+                for (int h = 0; h < H; ++h) {
+                    o[h] = j < 64 ? __shfl_xor(v[h], j, 64) : v[h ^ (j >> 6)];
+                }
+#pragma unroll
+                for (int h = 0; h < H; ++h) {
+                    const int i = lane + 64 * h;
+                    const bool keep_min = ((i & j) == 0) == ((i & k) == 0);
+                    v[h] = keep_min ? fminf(v[h], o[h]) : fmaxf(v[h], o[h]);
+                }
+            }
+        }
+        const float last_index = (float)(n - 1);
+        for (int e0 = 0; e0 < n_entries; e0 += 64) {  // uniform: every lane shuffles
+            const int e = e0 + lane;
+            float rank, wt;
+            int lo, hi;
+            {
+                // each product and difference rounded on its own, as torch's
+                // CPU quantile computes them: no contraction into fma here
+#pragma clang fp contract(off)
+                rank = qf.q[e < n_entries ? e : 0] * last_index;
+                lo = (int)rank;
+                hi = (int)ceilf(rank);
+                wt = rank - (float)lo;
+            }
+            const float a = sorted_at<H>(v, lo), c = sorted_at<H>(v, hi);
+            const float r = fabsf(wt) < 0.5f ? __builtin_fmaf(wt, c - a, a)
+                                             : __builtin_fmaf(wt - 1.0f, c - a, c);
+            if (e < n_entries) cb[b * n_entries + e] = r;
+        }
+    }
+}
+
 template <bool kBF16>
 __global__ __launch_bounds__(kThreads) void dequant_kernel(
     const uint8_t* __restrict__ packed, int64_t nbytes,
@@ -559,6 +632,23 @@ int launch_block_codebooks(const float* w, int64_t total, int64_t num_blocks, in
     if (num_blocks == 0) return NB_OK;
     QuantileFractions qf;
     for (int e = 0; e < kCbMaxEntries; ++e) qf.q[e] = e < n_entries ? q[e] : 0.f;
+    if (block_size <= 256) {
+        const int64_t want = (num_blocks + kThreads / 64 - 1) / (kThreads / 64);
+        const int64_t cap = (int64_t)device_cu_count() * 16;
+        const int grid = (int)(want < cap ? want : cap);
+        auto go = [&](auto kernel) {
+            hipLaunchKernelGGL(kernel, dim3(grid), dim3(kThreads), 0, stream, w, total,
+                               num_blocks, block_size, n_entries, qf, cb);
+        };
+        if (block_size <= 64) {
+            go(block_codebooks_wave_kernel<1>);
+        } else if (block_size <= 128) {
+            go(block_codebooks_wave_kernel<2>);
+        } else {
+            go(block_codebooks_wave_kernel<4>);
+        }
+        return check_launch("nb_block_codebooks");
+    }
     int64_t grid = num_blocks;
     const int64_t cap = (int64_t)device_cu_count() * 32;
     if (grid > cap) grid = cap;
