@@ -317,16 +317,20 @@ def bench_prefill(dev, random_weights=False):
     for M in (512, 2048):
         xs = {K: synth.make_activation(K, m=M, seed=M + K, device=dev, dtype=torch.bfloat16)
               for K in (2560, 6912)}
-        per, tot_ms, tot_fl, ref_ms = {}, 0.0, 0, 0.0
+        per, tot_ms, tot_fl, ref_ms, fused_ms = {}, 0.0, 0, 0.0, 0.0
         for n, N, K in PREFILL_SHAPES:
             lay = layers[n]
             y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
             ms = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y), 20)
+            ms_fused = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K,
+                                                           out=y, path="fused"), 20)
             w = torch.empty(N, K, dtype=torch.bfloat16, device=dev).normal_()
             ms_ref = event_time(lambda: torch.matmul(xs[K], w.T), 20)
             fl = 2 * M * N * K
             per[n] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / ms / 1e9, 1),
+                      "fused_kernel_us": round(ms_fused * 1e3, 1),
                       "torch_dense_bf16_us": round(ms_ref * 1e3, 1)}
+            fused_ms = fused_ms + ms_fused
             tot_ms += ms
             ref_ms += ms_ref
             tot_fl += fl
@@ -335,11 +339,17 @@ def bench_prefill(dev, random_weights=False):
                         "TFLOP_s": round(tot_fl / tot_ms / 1e9, 1),
                         "pct_bf16_mfma_peak": round(tot_fl / tot_ms / 1e9 / 2500 * 100, 2),
                         "model_26_layers_ms": round(26 * tot_ms, 3),
+                        "path": "blas" if M >= ops.PREFILL_BLAS_MIN_ROWS else "fused",
+                        "fused_kernel_layer_us": round(fused_ms * 1e3, 1),
                         "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
                         "per_matmul": per}
-    out["note"] = ("nb_gemm_prefill reads the 3-bit stream and codebooks directly; torch_dense_bf16 "
-                   "is torch.matmul on an already-unpacked bf16 weight (the reference's path also "
-                   "unpacks and gathers W on every call, triton_kernel.py:258-275)")
+    out["note"] = ("us / TFLOP_s: ops.gemm_prefill's default path -- from 256 rows on "
+                   "nb_gemm_prefill_ws (W expanded to bf16 in a workspace by the format kernel, "
+                   "then one hipBLASLt GEMM; the expansion is inside the timed call); "
+                   "fused_kernel: nb_gemm_prefill, whose MFMA kernel reads the 3-bit stream and "
+                   "codebooks directly; torch_dense_bf16 is torch.matmul on an already-unpacked "
+                   "bf16 weight (the reference's path also unpacks and gathers W on every call, "
+                   "triton_kernel.py:258-275)")
     return out
 
 

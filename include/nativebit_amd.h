@@ -109,6 +109,22 @@ int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed, const flo
                     void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* stream);
 
 /*
+ * nb_gemm_prefill with a caller workspace (>= nb_gemm_prefill_ws_bytes(M, N,
+ * K) bytes, 256-byte aligned, contents clobbered): W is expanded to bf16 in
+ * the workspace by the format kernel and y = x . W^T is one hipBLASLt GEMM
+ * (bf16 operands, fp32 accumulation) -- faster than the fused kernel for
+ * many activation rows.  Same operands and result contract as
+ * nb_gemm_prefill; the fused kernel runs where the library has no algorithm.
+ * Replaces: the same batched branch of PackedLinear.forward in its bf16
+ *           form (inference/triton_kernel.py:258-275, inference/eval_ppl.py:
+ *           149-174: gather W, cast to bf16, dense matmul).
+ */
+int64_t nb_gemm_prefill_ws_bytes(int M, int N, int K);
+int nb_gemm_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                       void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
+                       int64_t ws_bytes, void* stream);
+
+/*
  * Unpack `count` indices of `bits` bits to one byte each.
  * Replaces: unpack_3bit / unpack_4bit / unpack_nbits
  *           (nativebit/pack.py:44-68, 85-90, 119-138) and

@@ -116,6 +116,18 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
 int launch_prefill(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
 
+// hipBLASLt's own share of the prefill workspace, after the bf16 weight.
+constexpr int64_t kPrefillBlasWorkspace = 32ll << 20;
+
+// Bytes of the bf16 weight copy at the start of the prefill workspace.
+int64_t prefill_ws_weight_bytes(int N, int K);
+
+// Dequantize W to bf16 in the workspace, then one hipBLASLt GEMM (the fused
+// kernel if the library has no algorithm for the shape).
+int launch_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                      void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
+                      int64_t ws_bytes, hipStream_t stream);
+
 // Decode-step kernels (nb_decode.hip).
 int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
                        const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream);

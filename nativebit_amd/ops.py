@@ -237,11 +237,20 @@ class GemvBatch:
                                                   self.m, _DT[self.y_dtype], stream))
 
 
+# activation rows from which gemm_prefill's "auto" path takes hipBLASLt
+PREFILL_BLAS_MIN_ROWS = 256
+
+
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
                  K: int, out_dtype: torch.dtype = torch.bfloat16,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
     """y = x @ bf16(W).T for a 3-bit / 8-entry / block-128 packed W (N x K);
-    x (M, K) bfloat16, row-contiguous, fp32 accumulation."""
+    x (M, K) bfloat16, row-contiguous, fp32 accumulation.
+
+    ``path``: "fused" (nb_gemm_prefill: dequantization inside the MFMA
+    kernel), "blas" (nb_gemm_prefill_ws: W expanded to bf16 in a workspace,
+    then one hipBLASLt GEMM) or "auto" (blas from PREFILL_BLAS_MIN_ROWS rows
+    on, where it measured faster)."""
     for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
         _require_cuda(name, t)
     _same_device(x, packed, codebook)
@@ -258,7 +267,17 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
         out = torch.empty((M, N), dtype=out_dtype, device=x.device)
     elif out.shape != (M, N) or out.dtype not in _DT or out.stride(1) != 1:
         raise ValueError("out must be (M, N), row-contiguous")
-    _lib.check(_lib.load().nb_gemm_prefill(
+    if path not in ("auto", "fused", "blas"):
+        raise ValueError(f"unknown prefill path {path!r}")
+    lib = _lib.load()
+    if path == "blas" or (path == "auto" and M >= PREFILL_BLAS_MIN_ROWS):
+        nbytes = int(lib.nb_gemm_prefill_ws_bytes(M, N, K))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        _lib.check(lib.nb_gemm_prefill_ws(
+            x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
+            _DT[out.dtype], out.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x)))
+        return out
+    _lib.check(lib.nb_gemm_prefill(
         x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
         _DT[out.dtype], out.stride(0), M, N, K, _stream(x)))
     return out

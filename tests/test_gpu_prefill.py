@@ -38,12 +38,13 @@ def layer(N, K, seed):
                                    (17, 2560, 2560), (512, 2560, 2560), (300, 7680, 2560),
                                    (64, 2560, 6912)])
 @pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])
-def test_prefill_vs_f64(dev, M, N, K, ydt):
-    note(f"prefill M={M} N={N} K={K} {ydt}")
+@pytest.mark.parametrize("path", ["fused", "blas"])
+def test_prefill_vs_f64(dev, M, N, K, ydt, path):
+    note(f"prefill M={M} N={N} K={K} {ydt} {path}")
     idx, p, cb = layer(N, K, M * 7 + N)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + N)).to(torch.bfloat16)
     xd, pd, cd = x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
-    y = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=ydt)
+    y = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=ydt, path=path)
     w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
     w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
     # fp64 brute force on row subsets for the large shapes (keeps the CPU time short)
@@ -53,14 +54,15 @@ def test_prefill_vs_f64(dev, M, N, K, ydt):
     assert rel(got, ref) <= (1e-3 if ydt == torch.float32 else 1e-2), rel(got, ref)
 
 
-def test_prefill_strided_x_and_out(dev):
+@pytest.mark.parametrize("path", ["fused", "blas"])
+def test_prefill_strided_x_and_out(dev, path):
     M, N, K = 96, 256, 512
     idx, p, cb = layer(N, K, 5)
     big = torch.randn(M, K + 64).to(torch.bfloat16).to(dev)
     x = big[:, :K]                      # row stride K + 64 (a multiple of 8)
     out = torch.full((M, N + 8), float("nan"), device=dev)[:, :N]
     ops.gemm_prefill(x, torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K,
-                     out=out)
+                     out=out, path=path)
     w = torch.from_numpy(O.dequant(idx, cb, 128, N * K).reshape(N, K)).to(torch.bfloat16).float()
     ref = x.float().cpu() @ w.T
     assert rel(out.cpu(), ref) <= 1e-5
@@ -81,6 +83,19 @@ def test_prefill_deterministic(dev):
     idx, p, cb = layer(2560, 2560, 9)
     x = torch.randn(256, 2560).to(torch.bfloat16).to(dev)
     pd, cd = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
-    a = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32)
-    b = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32)
+    a = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32, path="fused")
+    b = ops.gemm_prefill(x, pd, cd, 2560, 2560, out_dtype=torch.float32, path="fused")
     assert torch.equal(a, b)
+
+
+def test_prefill_paths_agree(dev):
+    """The workspace path (bf16 W in a workspace, hipBLASLt GEMM) and the
+    fused kernel multiply the same bf16 operands with fp32 accumulation:
+    they agree to fp32 summation-order differences."""
+    lay = synth.make_layer(2560, 6912, seed=13, device=dev)
+    x = synth.make_activation(6912, m=512, seed=14, device=dev, dtype=torch.bfloat16)
+    a = ops.gemm_prefill(x, lay.packed, lay.codebook, 2560, 6912, out_dtype=torch.float32,
+                         path="fused")
+    b = ops.gemm_prefill(x, lay.packed, lay.codebook, 2560, 6912, out_dtype=torch.float32,
+                         path="blas")
+    assert rel(a.cpu(), b.cpu()) <= 1e-5, rel(a.cpu(), b.cpu())
