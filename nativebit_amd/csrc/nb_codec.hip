@@ -470,6 +470,14 @@ __global__ __launch_bounds__(kThreads) void pack_chunks_kernel(
     }
 }
 
+// Two finite fp32 values rounded to bf16 (nearest, ties to even), packed low
+// | high: gfx950 converts a pair in one instruction (v_cvt_pk_bf16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2_rne(float lo, float hi) {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 // block_size % 32 == 0, so a chunk lies inside one block.
 template <int BITS, bool kBF16>
 __global__ __launch_bounds__(kThreads) void dequant_chunks_kernel(
@@ -495,10 +503,7 @@ __global__ __launch_bounds__(kThreads) void dequant_chunks_kernel(
             if (kBF16) {
                 uint32_t h[4];
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    h[k] = (uint32_t)f32_to_bf16_rne(v[8 * q + 2 * k]) |
-                           ((uint32_t)f32_to_bf16_rne(v[8 * q + 2 * k + 1]) << 16);
-                }
+                for (int k = 0; k < 4; ++k) h[k] = pack_bf16x2_rne(v[8 * q + 2 * k], v[8 * q + 2 * k + 1]);
                 pc[q] = make_uint4(h[0], h[1], h[2], h[3]);
             } else {
                 pc[q] = make_uint4(__float_as_uint(v[4 * q]), __float_as_uint(v[4 * q + 1]),
