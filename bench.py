@@ -436,7 +436,7 @@ def bench_config0(dev, cpu=True):
 
 
 def bench_quantize(dev):
-    """Quantize-at-pack on the GPU (SURVEY next row 4): nearest-entry
+    """Quantize-at-pack on the GPU (inference/pack.py:21-57): nearest-entry
     indices of a 6912x2560 fp32 weight against its per-block quantile
     codebooks, packed to the 3-bit stream by one kernel (nb_quantize_pack),
     beside the reference's formulation on the same device (a dense

@@ -67,7 +67,7 @@ HAND = [
     ("8bit_bytes", 8, [0, 255, 128], "00ff80"),
 ]
 
-# Packed lengths from the padding rules (SURVEY-independent: written from the
+# Packed lengths from the padding rules (written independently from the
 # rules quoted above).
 LENGTHS = [
     (3, 1, 3), (3, 8, 3), (3, 10, 6), (3, 1001, 378), (3, 100000, 37500),
