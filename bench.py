@@ -339,13 +339,14 @@ def bench_prefill(dev, random_weights=False):
                         "TFLOP_s": round(tot_fl / tot_ms / 1e9, 1),
                         "pct_bf16_mfma_peak": round(tot_fl / tot_ms / 1e9 / 2500 * 100, 2),
                         "model_26_layers_ms": round(26 * tot_ms, 3),
-                        "path": "blas" if M >= ops.PREFILL_BLAS_MIN_ROWS else "fused",
+                        "paths": {n: "blas" if ops.prefill_uses_blas(M, N, K) else "fused"
+                                  for n, N, K in PREFILL_SHAPES},
                         "fused_kernel_layer_us": round(fused_ms * 1e3, 1),
                         "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
                         "per_matmul": per}
-    out["note"] = ("us / TFLOP_s: ops.gemm_prefill's default path -- from 256 rows on "
-                   "nb_gemm_prefill_ws (W expanded to bf16 in a workspace by the format kernel, "
-                   "then one hipBLASLt GEMM; the expansion is inside the timed call); "
+    out["note"] = ("us / TFLOP_s: ops.gemm_prefill's default path per shape ('paths': blas = "
+                   "nb_gemm_prefill_ws, W expanded to bf16 in a workspace by the format kernel, "
+                   "then one hipBLASLt GEMM, the expansion inside the timed call); "
                    "fused_kernel: nb_gemm_prefill, whose MFMA kernel reads the 3-bit stream and "
                    "codebooks directly; torch_dense_bf16 is torch.matmul on an already-unpacked "
                    "bf16 weight (the reference's path also unpacks and gathers W on every call, "

@@ -237,8 +237,15 @@ class GemvBatch:
                                                   self.m, _DT[self.y_dtype], stream))
 
 
-# activation rows from which gemm_prefill's "auto" path takes hipBLASLt
-PREFILL_BLAS_MIN_ROWS = 256
+def prefill_uses_blas(M: int, N: int, K: int) -> bool:
+    """gemm_prefill's "auto" choice, from per-shape timings of both paths on
+    MI355X (M = 64..2048 on the 2.2B shapes): the workspace path wins for
+    long rows (K > 4096: the fused kernel has too few output tiles), small
+    matrices (N*K <= 8M: the bf16 expansion is cheap) and many rows; the
+    fused kernel wins for the wide K = 2560 shapes at a few hundred rows."""
+    if K > 4096 or N * K <= (8 << 20) or M >= 1024:
+        return True
+    return M >= 384 and N >= 10000
 
 
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
@@ -249,8 +256,7 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
 
     ``path``: "fused" (nb_gemm_prefill: dequantization inside the MFMA
     kernel), "blas" (nb_gemm_prefill_ws: W expanded to bf16 in a workspace,
-    then one hipBLASLt GEMM) or "auto" (blas from PREFILL_BLAS_MIN_ROWS rows
-    on, where it measured faster)."""
+    then one hipBLASLt GEMM) or "auto" (prefill_uses_blas)."""
     for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
         _require_cuda(name, t)
     _same_device(x, packed, codebook)
@@ -270,7 +276,7 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
     if path not in ("auto", "fused", "blas"):
         raise ValueError(f"unknown prefill path {path!r}")
     lib = _lib.load()
-    if path == "blas" or (path == "auto" and M >= PREFILL_BLAS_MIN_ROWS):
+    if path == "blas" or (path == "auto" and prefill_uses_blas(M, N, K)):
         nbytes = int(lib.nb_gemm_prefill_ws_bytes(M, N, K))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         _lib.check(lib.nb_gemm_prefill_ws(
