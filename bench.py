@@ -147,13 +147,42 @@ def build_model(dev, n_layers, random_weights=False):
     return layers
 
 
-def graph_time(run, steps, warmup):
-    """Captures run() once in a HIP graph; returns ms per replay."""
+# GPU time spent running the timed work back to back, untimed, before its
+# warm-up steps.  On MI355X a memory-bound load that starts on an idle GPU
+# runs its first ~1 ms at full clocks, then the power controller
+# over-corrects for ~20 ms (the same launch takes up to 1.45x as long), then
+# settles; an idle gap of a millisecond starts the cycle over.  Timing a few
+# replays right after the warm-up would measure that transient, not the
+# kernel, so every timed region here starts after this much continuous work
+# (the transient itself is reported beside the headline number).
+SETTLE_S = 0.15
+
+
+def _settle(fn, seconds=SETTLE_S, cap=20000):
+    """Runs fn() back to back for about `seconds` of GPU time (the count
+    from one timed call), without host synchronisation in between."""
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    fn()
+    e.record()
+    torch.cuda.synchronize()
+    per_ms = max(s.elapsed_time(e), 1e-3)
+    n = int(min(cap, max(1, seconds * 1e3 / per_ms)))
+    for _ in range(n):
+        fn()
+    return n + 1
+
+
+def graph_time(run, steps, warmup, settle_s=SETTLE_S, info=None):
+    """Captures run() once in a HIP graph; returns ms per replay over
+    `steps` timed replays, after `settle_s` seconds of untimed replays and
+    `warmup` untimed replays (see SETTLE_S)."""
     run()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         run()
+    n_settle = _settle(g.replay, settle_s) if settle_s > 0 else 0
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -163,7 +192,25 @@ def graph_time(run, steps, warmup):
         g.replay()
     end.record()
     torch.cuda.synchronize()
+    if info is not None:
+        info["settle_replays"] = n_settle
+        info["graph"] = g
     return start.elapsed_time(end) / steps
+
+
+def transient_profile(g, idle_s=0.05, n=40):
+    """Per-replay times (us) of graph g replayed n times after the GPU has
+    idled for idle_s: the power controller's transient that SETTLE_S
+    keeps out of the timed regions."""
+    torch.cuda.synchronize()
+    time.sleep(idle_s)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record()
+    for i in range(n):
+        g.replay()
+        ev[i + 1].record()
+    torch.cuda.synchronize()
+    return [round(ev[i].elapsed_time(ev[i + 1]) * 1e3, 1) for i in range(n)]
 
 
 def copy_calibration(dev, steps, warmup):
@@ -229,12 +276,54 @@ def spot_check(mats):
     return worst
 
 
+def host_cpu():
+    """The host's CPU resources as this process sees them: the CPUs in its
+    affinity mask, the cgroup CPU quota (cpu.max), the physical cores behind
+    the affinity CPUs and the CPU model.  ``threads`` = the affinity count,
+    capped by the quota when one is set (more threads than the quota only
+    time-slice)."""
+    aff = sorted(os.sched_getaffinity(0))
+    quota = None
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            q, period = f.read().split()[:2]
+            if q != "max":
+                quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    model, cores, cur = "", set(), {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    cur = {"cpu": int(v)}
+                elif k in ("physical id", "core id"):
+                    cur[k] = v
+                elif k == "model name":
+                    model = model or v
+                if "core id" in cur and cur.get("cpu") in aff:
+                    cores.add((cur.get("physical id"), cur["core id"]))
+    except OSError:
+        pass
+    threads = min(len(aff), quota) if quota else len(aff)
+    return {"threads": threads, "affinity_cpus": len(aff), "cgroup_quota_cpus": quota,
+            "physical_cores": len(cores) or None, "model": model or platform.processor()}
+
+
+def _host_desc(h):
+    q = f", cgroup quota {h['cgroup_quota_cpus']} CPUs" if h["cgroup_quota_cpus"] else ""
+    return (f"{h['threads']} threads ({h['affinity_cpus']} CPUs in the affinity mask{q}, "
+            f"{h['physical_cores']} physical cores) of {h['model']}")
+
+
 def cpu_baseline(mats, reps, seconds):
     """The reference CPU path (unpack + gather + F.linear, restated in
     oracle.torch_packed_linear_f32) on layer 0's 7 matmuls."""
     from oracle import oracle as O
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(threads)
+    h = host_cpu()
+    torch.set_num_threads(h["threads"])
     host = [(m.x.float().cpu(), m.packed.cpu(), m.cb.cpu(), m.N, m.K) for m in mats]
     nbytes = sum(m.bytes for m in mats)
 
@@ -250,25 +339,22 @@ def cpu_baseline(mats, reps, seconds):
         once()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            cpu_model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
     return {
-        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": h["threads"], "kind": "port",
         "sample": (f"layer 0 of config 1 (q, k, v, o, gate, up, down; {nbytes} B): torch CPU "
                    f"unpack+gather+F.linear (reference triton_kernel.py:258-275), x bf16 upcast "
                    f"to fp32, median of {len(times)} passes ({sum(times):.1f} s) after 1 warm-up "
-                   f"= {t*1e3:.1f} ms per pass; {threads} "
-                   f"threads on {cpu_model or platform.processor()}"),
+                   f"= {t*1e3:.1f} ms per pass; {_host_desc(h)}"),
         "seconds_per_sample": round(t, 4),
+        "host": h,
     }
 
 
-def event_time(fn, reps, warmup=3):
-    """ms per call of fn() on the current stream (HIP events)."""
+def event_time(fn, reps, warmup=3, settle_s=SETTLE_S):
+    """ms per call of fn() on the current stream (HIP events), after
+    settle_s seconds of untimed calls (see SETTLE_S) and `warmup` more."""
+    if settle_s > 0:
+        _settle(fn, settle_s, cap=2000)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -417,7 +503,7 @@ def bench_config0(dev, cpu=True):
            "copies": copies, "kernel": "gemv_fast_kernel (fp32 x, exact fp32 codebook values)"}
     if cpu:
         from oracle import oracle as O
-        threads = max(1, min(16, len(os.sched_getaffinity(0))))
+        threads = host_cpu()["threads"]
         torch.set_num_threads(threads)
         xh, ph, ch = x.cpu(), lay.packed.cpu(), lay.codebook.cpu()
         O.torch_packed_linear_f32(xh, ph, ch, N, K, BS, BITS)
@@ -571,10 +657,13 @@ def main():
     results = {}
 
     batch = ops.GemvBatch([(m.x, m.packed, m.cb, m.y, m.N, m.K) for m in all_mats])
-    ms = graph_time(batch.run, args.steps, args.warmup)
+    ginfo = {}
+    ms = graph_time(batch.run, args.steps, args.warmup, info=ginfo)
+    transient = transient_profile(ginfo.pop("graph"))
     err = spot_check(all_mats[:7])
     results["batched"] = {"launches": 1, "us_per_step": round(ms * 1e3, 2),
-                          "GB_s": round(step_bytes / ms / 1e6, 1)}
+                          "GB_s": round(step_bytes / ms / 1e6, 1),
+                          "settle_replays": ginfo["settle_replays"]}
     log(f"[bench] batched  : 1 launch/step, {step_bytes} B, {ms*1e3:.1f} us/step, "
         f"{step_bytes/ms/1e6:.1f} GB/s ({step_bytes/ms/1e6/HBM_PEAK_GBS*100:.1f}% of 8 TB/s), "
         f"spot-check rel err {err:.2e}")
@@ -647,6 +736,15 @@ def main():
                        "per graph replay of the single launch, on the launch stream"),
         },
         "schedules": results,
+        "timing": {
+            "settle": (f"{ginfo['settle_replays']} untimed replays (~{SETTLE_S} s of GPU time) "
+                       f"before the {args.warmup} warm-up and {args.steps} timed replays"),
+            "after_idle_us_per_replay": transient,
+            "after_idle_note": ("the same graph replayed right after 50 ms of GPU idle: the "
+                                "first ~1 ms runs at full clocks, then the power controller "
+                                "throttles for ~20 ms before it settles; the timed region "
+                                "above starts after that"),
+        },
         "parity": {"spot_check_rel_err_vs_f64": err},
     }
     if not args.no_extra:

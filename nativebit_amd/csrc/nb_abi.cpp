@@ -658,7 +658,12 @@ extern "C" int nb_decode_persistent(const nb_decode_model* model, void* workspac
     if (n_steps == 0) return NB_OK;
     st = ensure_device();
     if (st) return st;
-    return launch_decode_persistent(*model, workspace, state, logits, tokens_out, tokens_cap, force,
-                                    n_force, n_steps, spin_limit > 0 ? spin_limit : (1 << 20),
-                                    static_cast<hipStream_t>(stream));
+    // The kernel made an illegal memory access on a 26-layer model in a
+    // 128-step launch and the cause has not been shown: it is not launched.
+    (void)logits;
+    (void)spin_limit;
+    (void)stream;
+    return fail(NB_EUNSUPPORTED,
+                "%s: switched off (an illegal memory access on a 26-layer model is not yet "
+                "explained); use the per-launch decode step", fn);
 }

@@ -166,9 +166,14 @@ class DecodeEngine(_DecoderBase):
     """Device-resident greedy decoder for one sequence (batch 1): one HIP
     graph of launches per token."""
 
-    def __init__(self, model: PackedGPT, max_steps: int | None = None):
+    def __init__(self, model: PackedGPT, max_steps: int | None = None,
+                 record_layers: bool = False):
+        """``record_layers``: after every layer the step also copies the
+        residual stream into ``self.layer_x[l]`` (for layer-by-layer
+        comparisons; one extra copy launch per layer)."""
         super().__init__(model, max_steps)
         C, F, H = self.C, self.F, self.H
+        self.layer_x = self._z(model.cfg.n_layers, C) if record_layers else None
         z, bf16 = self._z, torch.bfloat16
         self.x = z(C)                # residual stream (fp32)
         self.h = z(C, dt=bf16)       # normalised embedding row (layer 0) and final norm
@@ -221,6 +226,8 @@ class DecodeEngine(_DecoderBase):
             g_o.run()                        # x += W_o att
             g_gu.run()                       # gu = W_gu rmsnorm(x)
             g_d.run()                        # x += W_down (silu(gate) * up)
+            if self.layer_x is not None:
+                self.layer_x[l].copy_(self.x)
         ck(lib.nb_add_rmsnorm(_ptr(self.x), None, None, st, _ptr(self.ln_f), _ptr(self.h),
                               BF, C, self.eps, s))
         ck(lib.nb_lm_head_argmax(_ptr(self.h), _ptr(self.emb_bf16), _ptr(self.logits), st,
@@ -255,6 +262,10 @@ class PersistentDecodeEngine(_DecoderBase):
     of tokens per launch of nb_decode_persistent."""
 
     def __init__(self, model: PackedGPT, max_steps: int | None = None, spin_limit: int = 0):
+        raise _lib.NativeBitError(
+            _lib.NB_EUNSUPPORTED,
+            "PersistentDecodeEngine is switched off: nb_decode_persistent made an illegal "
+            "memory access on a 26-layer model whose cause is not yet shown; use DecodeEngine")
         super().__init__(model, max_steps)
         self.spin_limit = int(spin_limit)
         rows = []

@@ -99,3 +99,40 @@ def test_prefill_paths_agree(dev):
     b = ops.gemm_prefill(x, lay.packed, lay.codebook, 2560, 6912, out_dtype=torch.float32,
                          path="blas")
     assert rel(a.cpu(), b.cpu()) <= 1e-5, rel(a.cpu(), b.cpu())
+
+
+# Config 4a: M = 2048 tokens on the four matmul shapes of a 2.2B layer
+# (q|k|v, o, gate|up, down), every path, against the fp64 brute force on 24
+# rows spread over M.
+PREFILL_2P2B = {"qkv": (7680, 2560), "o": (2560, 2560), "gate|up": (13824, 2560),
+                "down": (2560, 6912)}
+_LAYER_CACHE = {}
+
+
+def _layer_2p2b(name):
+    if name not in _LAYER_CACHE:
+        N, K = PREFILL_2P2B[name]
+        idx, p, cb = layer(N, K, 4242 + N + K)
+        w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+        w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+        _LAYER_CACHE.clear()  # one shape at a time (the 13824 x 2560 weight is 142 MB)
+        _LAYER_CACHE[name] = (p, cb, w)
+    return _LAYER_CACHE[name]
+
+
+@pytest.mark.parametrize("ydt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("path", ["auto", "fused", "blas"])
+@pytest.mark.parametrize("name", list(PREFILL_2P2B))
+def test_prefill_m2048_2p2b(dev, name, path, ydt):
+    M = 2048
+    N, K = PREFILL_2P2B[name]
+    note(f"prefill M={M} {name} {N}x{K} {path} {ydt}")
+    p, cb, w = _layer_2p2b(name)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(N + K)).to(torch.bfloat16)
+    y = ops.gemm_prefill(x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev),
+                         N, K, out_dtype=ydt, path=path)
+    rows = np.unique(np.linspace(0, M - 1, 24).astype(int))
+    ref = O.matmul_f64(x.float().numpy()[rows], w)
+    got = y.float().cpu().numpy()[rows]
+    assert np.isfinite(got).all()
+    assert rel(got, ref) <= (1e-3 if ydt == torch.float32 else 1e-2), rel(got, ref)
