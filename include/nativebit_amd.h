@@ -308,6 +308,28 @@ int nb_attention_step(const float* qkv, float* k_cache, float* v_cache, const fl
 int nb_attention_work_floats(int n_head);
 
 /*
+ * nb_attention_step without the workspace: the same kernel and the same
+ * results, with the split partials and head counters in a static device
+ * array of the library (nb_attention_static_scratch_bytes() bytes, about
+ * 1 MiB, one copy on each GPU it runs on, held until the process ends) --
+ * the call allocates nothing (no hipMalloc, no library allocation).
+ * n_head <= 64; otherwise as nb_attention_step.  All calls on one GPU share
+ * that GPU's array: calls that overlap in time on one GPU (several streams
+ * or threads) race, and must be ordered by the caller.  The head counters
+ * start at zero (cleared once per device by a small kernel on the first
+ * call's stream) and every completed call leaves them at zero.
+ * No counterpart in the reference (whose attention is torch code,
+ * inference/generate_torch.py:72-106).  It is for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation.
+ */
+int nb_attention_step_static(const float* qkv, float* k_cache, float* v_cache,
+                             const float* cos_t, const float* sin_t,
+                             const nb_decode_state* state, void* out, int out_dtype,
+                             int n_head, int head_dim, int ctx, void* stream);
+int64_t nb_attention_static_scratch_bytes(void);
+
+/*
  * act[i] = silu(gu[i]) * gu[n + i]  (gu fp32 gate | up, act NB_F32/NB_BF16).
  * Replaces: F.silu(gate(x)) * up(x) (inference/generate_torch.py:116-117).
  */

@@ -67,6 +67,8 @@ SIGNATURES = {
     "nb_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P]),
     "nb_attention_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "nb_attention_work_floats": (_I, [_I]),
+    "nb_attention_step_static": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "nb_attention_static_scratch_bytes": (_L, []),
     "nb_silu_mul": (_I, [_P, _P, _I, _I, _P]),
     "nb_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
     "nb_decode_workspace_bytes": (_L, [_P]),

@@ -500,6 +500,44 @@ int nb_attention_step(const float* qkv, float* k_cache, float* v_cache, const fl
                                  out_dtype, n_head, head_dim, ctx, static_cast<hipStream_t>(stream));
 }
 
+int nb_attention_step_static(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                             const float* sin_t, const nb_decode_state* state, void* out,
+                             int out_dtype, int n_head, int head_dim, int ctx, void* stream) {
+    const char* fn = "nb_attention_step_static";
+    if (n_head < 1 || ctx < 1) return fail(NB_EINVAL, "%s: n_head=%d ctx=%d", fn, n_head, ctx);
+    if (n_head > static_attention_max_heads()) {
+        return fail(NB_EUNSUPPORTED, "%s: n_head=%d > %d (the library's static scratch holds "
+                    "%d heads; use nb_attention_step with a workspace)", fn, n_head,
+                    static_attention_max_heads(), static_attention_max_heads());
+    }
+    if (ctx > attention_max_ctx()) {
+        return fail(NB_EUNSUPPORTED, "%s: ctx=%d > %d", fn, ctx, attention_max_ctx());
+    }
+    if (head_dim < 2 || head_dim % 2 || head_dim > attention_max_head_dim()) {
+        return fail(NB_EUNSUPPORTED, "%s: head_dim=%d (even, <= %d)", fn, head_dim,
+                    attention_max_head_dim());
+    }
+    if (!qkv || !k_cache || !v_cache || !cos_t || !sin_t || !state || !out) {
+        return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    }
+    if (out_dtype != NB_F32 && out_dtype != NB_BF16) return fail(NB_EINVAL, "%s: out_dtype=%d", fn, out_dtype);
+    if (!aligned(qkv, 4) || !aligned(k_cache, 4) || !aligned(v_cache, 4) ||
+        !aligned(out, dtype_size(out_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    int st = ensure_device();
+    if (st) return st;
+    float* work = nullptr;
+    unsigned* done = nullptr;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    st = static_attention_scratch(s, &work, &done);
+    if (st) return st;
+    return launch_attention_step(qkv, k_cache, v_cache, cos_t, sin_t, state, work, done, out,
+                                 out_dtype, n_head, head_dim, ctx, s);
+}
+
+int64_t nb_attention_static_scratch_bytes(void) { return static_attention_scratch_bytes(); }
+
 int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream) {
     const char* fn = "nb_silu_mul";
     if (n < 1) return fail(NB_EINVAL, "%s: n=%d < 1", fn, n);

@@ -18,6 +18,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "nb_device.h"
 #include "nb_internal.h"
@@ -354,7 +355,62 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
     }
 }
 
+__global__ void zero_u32_kernel(unsigned* __restrict__ p, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free attention entry (nb_attention_step_static):
+// the split partials of up to kStaticAttnHeads heads, then one counter per
+// head, in a file-scope device array -- one copy on every GPU the library
+// runs on, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol): the device address comes from hipGetSymbolAddress, once per
+// device, with that device current.
+// ---------------------------------------------------------------------------
+constexpr int kStaticAttnHeads = 64;
+constexpr size_t kStaticAttnWorkBytes =
+    (size_t)kStaticAttnHeads * kAttnSplits * (kMaxHeadDim + 2) * sizeof(float);
+constexpr size_t kStaticAttnBytes = kStaticAttnWorkBytes + kStaticAttnHeads * sizeof(unsigned);
+static __device__ __align__(256) unsigned char scratch[kStaticAttnBytes];
+
+constexpr int kMaxScratchDevices = 64;
+unsigned char* g_scratch_ptr[kMaxScratchDevices];
+std::mutex g_scratch_mutex;
+
 }  // namespace
+
+int static_attention_max_heads() { return kStaticAttnHeads; }
+int64_t static_attention_scratch_bytes() { return (int64_t)kStaticAttnBytes; }
+
+int static_attention_scratch(hipStream_t stream, float** work, unsigned** done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess || dev < 0 || dev >= kMaxScratchDevices) {
+        return fail(NB_ENODEV, "nb_attention_step_static: no usable current device");
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            return fail(NB_ELAUNCH, "nb_attention_step_static: hipGetSymbolAddress failed: %s",
+                        hipGetErrorString(e));
+        }
+        // the head counters start at zero (every completed call leaves them
+        // at zero); cleared by a kernel on the caller's stream, once
+        hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, stream,
+                           reinterpret_cast<unsigned*>(static_cast<unsigned char*>(p) +
+                                                       kStaticAttnWorkBytes),
+                           kStaticAttnHeads);
+        const int st = check_launch("nb_attention_step_static");
+        if (st) return st;
+        g_scratch_ptr[dev] = static_cast<unsigned char*>(p);
+    }
+    *work = reinterpret_cast<float*>(g_scratch_ptr[dev]);
+    *done = reinterpret_cast<unsigned*>(g_scratch_ptr[dev] + kStaticAttnWorkBytes);
+    return NB_OK;
+}
 
 int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
                        const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream) {

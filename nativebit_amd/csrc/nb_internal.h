@@ -140,6 +140,11 @@ int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_deco
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                           int V, int C, hipStream_t stream);
 int attention_work_floats(int n_head);
+// The allocation-free attention's scratch on the current device (its
+// address from hipGetSymbolAddress, set up once per device).
+int static_attention_scratch(hipStream_t stream, float** work, unsigned** done);
+int static_attention_max_heads();
+int64_t static_attention_scratch_bytes();
 
 // Persistent decode (nb_decode_persistent.hip); arguments validated.
 int64_t decode_persistent_workspace_bytes(int C, int H, int F);

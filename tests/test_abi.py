@@ -356,6 +356,32 @@ def test_attention_step_validation(kw, status):
 
 
 @pytest.mark.parametrize("kw,status", [
+    (dict(n_head=65), _lib.NB_EUNSUPPORTED),       # beyond the static scratch
+    (dict(head_dim=127), _lib.NB_EUNSUPPORTED),
+    (dict(ctx=2048), _lib.NB_EUNSUPPORTED),
+    (dict(n_head=0), _lib.NB_EINVAL),
+    (dict(qkv=None), _lib.NB_EINVAL),
+    (dict(out_dtype=9), _lib.NB_EINVAL),
+    (dict(v_cache=FAKE + 2), _lib.NB_EALIGN),
+])
+def test_attention_step_static_validation(kw, status):
+    a = dict(qkv=FAKE, k_cache=FAKE, v_cache=FAKE, cos=FAKE, sin=FAKE, state=FAKE, out=FAKE,
+             out_dtype=_lib.NB_BF16, n_head=20, head_dim=128, ctx=1024, stream=None)
+    a.update(kw)
+    assert _lib.load().nb_attention_step_static(*a.values()) == status
+
+
+def test_attention_static_scratch_size():
+    lib = _lib.load()
+    # 64 heads of split partials (nb_attention_work_floats) + 64 counters
+    assert lib.nb_attention_static_scratch_bytes() == lib.nb_attention_work_floats(64) * 4 + 64 * 4
+    if not gpu_available():
+        a = dict(qkv=FAKE, k_cache=FAKE, v_cache=FAKE, cos=FAKE, sin=FAKE, state=FAKE, out=FAKE,
+                 out_dtype=_lib.NB_BF16, n_head=20, head_dim=128, ctx=1024, stream=None)
+        assert lib.nb_attention_step_static(*a.values()) == _lib.NB_ENODEV
+
+
+@pytest.mark.parametrize("kw,status", [
     (dict(C=100), _lib.NB_EUNSUPPORTED),
     (dict(C=16384), _lib.NB_EUNSUPPORTED),
     (dict(V=0), _lib.NB_EUNSUPPORTED),
