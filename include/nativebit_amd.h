@@ -214,12 +214,16 @@ int nb_dequant(const uint8_t* packed, const float* codebook, void* w_out,
  *                  (SwiGLU, inference/generate_torch.py:116-117).
  * y_mode: NB_Y_STORE writes y = result; NB_Y_ADD updates y[n] += result in
  * fp32 (y_dtype NB_F32 only; the residual adds of TransformerBlock.forward,
- * inference/generate_torch.py:128-132).  The y of an NB_Y_ADD item must not
- * overlap any x or norm_w of the same batch.  Zero-filled new fields select
- * the plain GEMV.
+ * inference/generate_torch.py:128-132); NB_Y_SILU_PAIRS takes the rows as
+ * (gate, up) pairs -- row 2i a gate row, row 2i+1 the up row of the same
+ * output -- and writes N/2 bf16 values y[i] = silu(r[2i]) * r[2i+1] from
+ * the fp32 row results r (SwiGLU's product, generate_torch.py:116-117, fed
+ * to the down projection; y_dtype NB_BF16, N even, the item alone in its
+ * batch).  The y of an NB_Y_ADD item must not overlap any x or norm_w of
+ * the same batch.  Zero-filled new fields select the plain GEMV.
  */
 enum nb_x_mode { NB_X_BF16 = 0, NB_X_RMSNORM = 1, NB_X_SILU_MUL = 2 };
-enum nb_y_mode { NB_Y_STORE = 0, NB_Y_ADD = 1 };
+enum nb_y_mode { NB_Y_STORE = 0, NB_Y_ADD = 1, NB_Y_SILU_PAIRS = 2 };
 typedef struct nb_batch_item {
     const void* x;          /* activations, see x_mode                     */
     const uint8_t* packed;  /* 3-bit stream of N*K indices                 */

@@ -39,6 +39,7 @@ NB_X_RMSNORM = 1
 NB_X_SILU_MUL = 2
 NB_Y_STORE = 0
 NB_Y_ADD = 1
+NB_Y_SILU_PAIRS = 2
 
 ABI_VERSION = 2
 

@@ -340,8 +340,17 @@ int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* 
         if (it.x_mode < NB_X_BF16 || it.x_mode > NB_X_SILU_MUL) {
             return fail(NB_EINVAL, "%s: item %d x_mode=%d", fn, i, it.x_mode);
         }
-        if (it.y_mode != NB_Y_STORE && it.y_mode != NB_Y_ADD) {
+        if (it.y_mode != NB_Y_STORE && it.y_mode != NB_Y_ADD && it.y_mode != NB_Y_SILU_PAIRS) {
             return fail(NB_EINVAL, "%s: item %d y_mode=%d", fn, i, it.y_mode);
+        }
+        if (it.y_mode == NB_Y_SILU_PAIRS) {
+            if (count != 1) {
+                return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_SILU_PAIRS must be alone in its "
+                            "batch (count=%d)", fn, i, count);
+            }
+            if (it.N % 2) {
+                return fail(NB_EINVAL, "%s: item %d NB_Y_SILU_PAIRS with odd N=%d", fn, i, it.N);
+            }
         }
         if (it.reserved != 0) return fail(NB_EINVAL, "%s: item %d reserved field not zero", fn, i);
         if (it.x_mode == NB_X_RMSNORM) {
@@ -406,12 +415,19 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
         if (items[i].y_mode == NB_Y_ADD && y_dtype != NB_F32) {
             return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_ADD needs fp32 outputs", fn, i);
         }
+        if (items[i].y_mode == NB_Y_SILU_PAIRS && y_dtype != NB_BF16) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_SILU_PAIRS needs bf16 outputs", fn, i);
+        }
     }
     st = ensure_device();
     if (st) return st;
     // host copy of the table the caller uploaded (same items, same order)
     std::vector<StreamProblem> host((size_t)nprob);
     build_stream_table(items, count, host.data());
+    if (host[0].y_mode == NB_Y_SILU_PAIRS && !gemv_rows_fits(host[0])) {
+        return fail(NB_EUNSUPPORTED, "%s: NB_Y_SILU_PAIRS item does not fit the single-problem "
+                    "kernel's LDS", fn);
+    }
     return launch_gemv_stream(static_cast<const StreamProblem*>(table_dev), host.data(), nprob,
                               y_dtype, static_cast<hipStream_t>(stream));
 }
@@ -434,6 +450,9 @@ int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, in
         ++nprob;
         if (items[i].x_mode != NB_X_BF16) {
             return fail(NB_EUNSUPPORTED, "%s: item %d: only NB_X_BF16 activations", fn, i);
+        }
+        if (items[i].y_mode == NB_Y_SILU_PAIRS) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d: NB_Y_SILU_PAIRS is for M = 1", fn, i);
         }
         if (y_dtype == NB_F32 && !aligned(items[i].y, 4)) {
             return fail(NB_EALIGN, "%s: item %d y not 4-byte aligned", fn, i);

@@ -248,6 +248,174 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     if (tid == 0) done[hd] = 0u;  // ready for the next step
 }
 
+// The same step for head_dim <= 128 with every global load of a workgroup
+// issued before the first is used: the query/key/value of the head and the
+// RoPE row first, then all of the split's cached keys (lane = position,
+// wave = a quarter of the dimensions, up to 32 loads per thread) and values
+// (thread = dimension and half of the positions, up to 32 loads), so a
+// workgroup pays one memory latency instead of one per dependent loop.
+// Scores, softmax partials, the weighted values and the split combine are
+// those of attention_step_kernel, in the same order.
+constexpr int kAttn2MaxD = 128;
+
+__global__ __launch_bounds__(kAttnThreads) void attention_step2_kernel(
+    const float* __restrict__ qkv, float* __restrict__ k_cache, float* __restrict__ v_cache,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const nb_decode_state* __restrict__ st, float* __restrict__ work, unsigned* __restrict__ done,
+    void* __restrict__ out, int out_dtype, int n_head, int D, int ctx) {
+    __shared__ float q[kAttn2MaxD], kn[kAttn2MaxD], vn[kAttn2MaxD];
+    __shared__ float sc[kAttnThreads / 64][kAttnMaxSplitLen];
+    __shared__ float p[kAttnMaxSplitLen];
+    __shared__ float oh[2][kAttn2MaxD];
+    __shared__ float ml[2];
+    __shared__ unsigned last;
+    const int hd = blockIdx.x, s = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = st->pos;
+    if (pos < 0 || pos >= ctx) return;  // past the cache: nothing to do
+    const int C = n_head * D;
+    const float scale = 1.0f / sqrtf((float)D);
+    const int n = pos + 1;
+    const int Lp = (n + kAttnSplits - 1) / kAttnSplits;
+    const int t0 = min(n, s * Lp), t1 = min(n, t0 + Lp);
+    const int len = t1 - t0;
+
+    // ---- loads: the head's new q, k, v and the RoPE row, then the split's
+    //      cached keys and values (clamped addresses; unused values are
+    //      never read)
+    const int half = D / 2;
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, c = 0.f, sn = 0.f, v0 = 0.f;
+    if (tid < half) {
+        q0 = qkv[hd * D + 2 * tid];
+        q1 = qkv[hd * D + 2 * tid + 1];
+        k0 = qkv[C + hd * D + 2 * tid];
+        k1 = qkv[C + hd * D + 2 * tid + 1];
+        c = cos_t[(int64_t)pos * half + tid];
+        sn = sin_t[(int64_t)pos * half + tid];
+    }
+    if (tid < D) v0 = qkv[2 * C + hd * D + tid];
+    const int dq = (D + 3) / 4;
+    const int d0 = wave * dq;
+    const int t = t0 + lane;
+    const int tk = lane < len ? t : t0;           // a position of the split
+    float kr[kAttn2MaxD / 4];
+    const float* kt = k_cache + (int64_t)hd * D * ctx;  // [D][ctx]
+    // values: thread (vh, d), vh = tid / 128: positions of half vh
+    const int vd = tid & (kAttn2MaxD - 1), vh = tid >> 7;
+    const int vlen = (len + 1) / 2;
+    const int vt0 = t0 + vh * vlen;
+    const int vcnt = max(0, min(vlen, t1 - vt0));
+    float vr[kAttnMaxSplitLen / 2];
+    const float* vc = v_cache + (int64_t)hd * ctx * D;  // [ctx][D]
+    if (len > 0) {
+#pragma unroll
+        for (int j = 0; j < kAttn2MaxD / 4; ++j) {
+            const int d = min(d0 + j, D - 1);
+            kr[j] = kt[(int64_t)d * ctx + tk];
+        }
+        const int dv = min(vd, D - 1);
+#pragma unroll
+        for (int j = 0; j < kAttnMaxSplitLen / 2; ++j) {
+            const int tt = min(vt0 + j, t1 - 1);
+            vr[j] = vc[(int64_t)tt * D + dv];
+        }
+    }
+    // RoPE of the new query and key (pairs (2i, 2i+1) rotated by angle i),
+    // then the reference's (q * scale)
+    if (tid < half) {
+        q[2 * tid] = __fmul_rn(__fadd_rn(__fmul_rn(q0, c), __fmul_rn(-q1, sn)), scale);
+        q[2 * tid + 1] = __fmul_rn(__fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, sn)), scale);
+        kn[2 * tid] = __fadd_rn(__fmul_rn(k0, c), __fmul_rn(-k1, sn));
+        kn[2 * tid + 1] = __fadd_rn(__fmul_rn(k1, c), __fmul_rn(k0, sn));
+    }
+    if (tid < D) vn[tid] = v0;
+    __syncthreads();
+    if (pos >= t0 && pos < t1 && tid < D) {
+        k_cache[((int64_t)hd * D + tid) * ctx + pos] = kn[tid];
+        v_cache[((int64_t)hd * ctx + pos) * D + tid] = vn[tid];
+    }
+    // partial scores of this wave's quarter of the dimensions
+    float part = 0.f;
+    if (lane < len) {
+        const bool is_new = t == pos;
+#pragma unroll
+        for (int j = 0; j < kAttn2MaxD / 4; ++j) {
+            if (j < dq && d0 + j < D) part += q[d0 + j] * (is_new ? kn[d0 + j] : kr[j]);
+        }
+    }
+    sc[wave][lane] = part;
+    __syncthreads();
+    float* wk = work + ((int64_t)hd * kAttnSplits + s) * (kMaxHeadDim + 2);
+    if (wave == 0) {
+        float score = -INFINITY;
+        if (lane < len) {
+            score = 0.f;
+            for (int w = 0; w < kAttnThreads / 64; ++w) score += sc[w][lane];
+        }
+        const float m = wave_max(score);
+        const float e = lane < len ? __expf(score - m) : 0.f;
+        const float l = wave_sum(e);
+        p[lane] = e;
+        if (lane == 0) {
+            ml[0] = m;
+            ml[1] = l;
+        }
+    }
+    __syncthreads();
+    // weighted values: thread (vh, vd) over its half of the positions
+    float o = 0.f;
+    if (vd < D) {
+#pragma unroll
+        for (int j = 0; j < kAttnMaxSplitLen / 2; ++j) {
+            if (j < vcnt) {
+                const int tt = vt0 + j;
+                o += p[tt - t0] * (tt == pos ? vn[vd] : vr[j]);
+            }
+        }
+    }
+    oh[vh][vd] = o;
+    __syncthreads();
+    if (tid < D) put_agent(wk + 2 + tid, oh[0][tid] + oh[1][tid]);
+    if (tid == 0) {
+        put_agent(wk, ml[0]);
+        put_agent(wk + 1, ml[1]);
+    }
+    // the last workgroup of this head combines the splits
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) {
+        last = __hip_atomic_fetch_add(done + hd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       kAttnSplits - 1
+                   ? 1u
+                   : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
+    if (tid < D) {
+        float M = -INFINITY;
+        float mj[kAttnSplits], lj[kAttnSplits], oj[kAttnSplits];
+#pragma unroll
+        for (int j = 0; j < kAttnSplits; ++j) {
+            const float* pj = base + j * (kMaxHeadDim + 2);
+            mj[j] = get_agent(pj);
+            lj[j] = get_agent(pj + 1);
+            oj[j] = get_agent(pj + 2 + tid);
+        }
+#pragma unroll
+        for (int j = 0; j < kAttnSplits; ++j) M = fmaxf(M, mj[j]);
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int j = 0; j < kAttnSplits; ++j) {
+            const float f = mj[j] == -INFINITY ? 0.f : __expf(mj[j] - M);
+            L += f * lj[j];
+            O += f * oj[j];
+        }
+        store_act(out, out_dtype, hd * D + tid, O / L);
+    }
+    if (tid == 0) done[hd] = 0u;  // ready for the next step
+}
+
 // ---------------------------------------------------------------------------
 // silu(gate) * up
 // ---------------------------------------------------------------------------
@@ -423,9 +591,15 @@ int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, cons
                           const float* sin_t, const nb_decode_state* st, float* work,
                           unsigned* done, void* out, int out_dtype, int n_head, int head_dim,
                           int ctx, hipStream_t stream) {
-    hipLaunchKernelGGL(attention_step_kernel, dim3(n_head, kAttnSplits), dim3(kAttnThreads), 0,
-                       stream, qkv, k_cache, v_cache, cos_t, sin_t, st, work, done, out, out_dtype,
-                       n_head, head_dim, ctx);
+    if (head_dim <= kAttn2MaxD) {
+        hipLaunchKernelGGL(attention_step2_kernel, dim3(n_head, kAttnSplits), dim3(kAttnThreads),
+                           0, stream, qkv, k_cache, v_cache, cos_t, sin_t, st, work, done, out,
+                           out_dtype, n_head, head_dim, ctx);
+    } else {
+        hipLaunchKernelGGL(attention_step_kernel, dim3(n_head, kAttnSplits), dim3(kAttnThreads),
+                           0, stream, qkv, k_cache, v_cache, cos_t, sin_t, st, work, done, out,
+                           out_dtype, n_head, head_dim, ctx);
+    }
     return check_launch("nb_attention_step");
 }
 

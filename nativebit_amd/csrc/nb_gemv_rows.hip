@@ -1,0 +1,370 @@
+// Single-problem streaming GEMV for the launches of a decode step (gfx950).
+//
+//   r[n] = sum_k a[k] * bf16(W[n][k])        (M = 1, 3-bit, 8 entries, BS 128)
+//
+// with a = x (bf16), RMSNorm(x) or silu(gate) * up (fp32 inputs, rounded to
+// bf16 once), as the batched kernel's x_mode forms, and y = r, y += r, or --
+// for a gate|up layer whose rows alternate gate, up -- y[i] =
+// bf16(silu(r[2i]) * r[2i+1]), the SwiGLU product the down projection reads
+// (NB_Y_SILU_PAIRS).  A decode step's GEMVs are 2-18 MB each, so a launch
+// lasts a few microseconds and its cost is latency, not bandwidth.  This
+// kernel is shaped for that:
+//
+// * Chunks are whole rows: R = floor(64 / bpr) rows (R * bpr <= 64 blocks,
+//   one block per lane), so any chunk range is row-aligned and every CU gets
+//   a share of even the smallest layer (a 2560 x 2560 o projection is 853
+//   chunks; the batched kernel's row-aligned tiles of 64-block chunks leave
+//   it 160 workgroups, and the 2560 x 6912 down projection 80).
+// * One workgroup per CU, 8 waves; a workgroup's chunks are dealt to its
+//   waves in turn, and each wave requests up to SLOTS of its chunks
+//   (direct-to-LDS, five 1 KiB loads each) at once.
+// * The activation inputs also arrive by direct-to-LDS loads, issued before
+//   the weight loads: vmcnt counts in issue order, so the wait for them
+//   leaves the weight loads in flight, and no compiler-tracked load sits
+//   among the ring loads (the compiler cannot see the ring loads and would
+//   otherwise wait for all of them).  The norm's sum of squares, the bf16
+//   rounding and the staging into the selector layout overlap the weights'
+//   arrival.
+// * Row sums in block order through a per-wave LDS scratch (deterministic,
+//   independent of the grid); y is written after the wave's last chunk.
+//
+// Weights are the codebook entries rounded to bf16 (RNE), as the reference's
+// bf16 path (inference/eval_ppl.py:149-174); accumulation is fp32.
+#include <algorithm>
+
+#include "nb_device.h"
+#include "nb_internal.h"
+#include "nb_stream_common.h"
+
+namespace nb {
+namespace {
+
+using namespace stream;
+
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSlotIdx = 64 * 48;                 // 3 KiB of index stream
+constexpr int kSlotBytes = kSlotIdx + 64 * 32;    // + 2 KiB of codebook
+constexpr int kLoads = 5;                         // dma16 per chunk
+constexpr int kMaxK = 8192;
+
+struct RowsArgs {
+    const uint8_t* packed;
+    const float* codebook;
+    const void* x;
+    const float* norm_w;
+    void* y;
+    int N, K, bpr, R, nchunks;
+    int unit;           // chunks per scheduling unit (2 keeps gate|up pairs in one wave)
+    int rows_per_wave;  // LDS row sums per wave
+    int raw_bytes;      // LDS bytes of the raw activation inputs (multiple of 1 KiB)
+    int y_mode, y_dtype;
+    float eps;
+};
+
+__device__ __forceinline__ float wsum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Halfword position of element e (0..7) of 8-element group g (0..15) of a
+// column block in the staged layout of nb_stream_common.h (stage_unit).
+__device__ __forceinline__ int staged_half(int g, int e) {
+    const int s = e == 0 ? 0 : e == 1 ? 1 : e == 2 ? 6 : e == 3 ? 2 : e == 4 ? 3 : e == 5 ? 7
+                : e == 6 ? 4 : 5;
+    return (4 * (g >> 2) + (s >> 1)) * 8 + (s & 1) * 4 + (g & 3);
+}
+
+// Waits until at most n loads are outstanding (n a multiple of kLoads, at
+// most N), with n as the instruction's immediate.
+template <int N>
+__device__ __forceinline__ void wait_vm_n(int n) {
+    if constexpr (N > 0) {
+        if (n >= N) {
+            wait_vm<N>();
+            return;
+        }
+        wait_vm_n<N - kLoads>(n);
+    } else {
+        wait_vm<0>();
+    }
+}
+
+// One 1 KiB piece of a contiguous byte range [base, base + nbytes) to LDS:
+// lane i copies bytes 16 i .. 16 i + 15 of piece p (past the end it re-reads
+// the range's last 16 bytes; those LDS bytes are never used).
+__device__ __forceinline__ void dma_piece(uint32_t lds, const uint8_t* base, int nbytes, int p,
+                                          int lane) {
+    const uint8_t* last = base + nbytes - 16;
+    const uint8_t* src = base + p * 1024 + 16 * lane;
+    dma16<0>(__builtin_amdgcn_readfirstlane(lds + p * 1024), src < last ? src : last);
+}
+
+template <int XMODE, int SLOTS>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemv_rows_kernel(RowsArgs a) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int K = a.K, bpr = a.bpr, R = a.R;
+    unsigned char* xs = smem;                                   // staged bf16 activations
+    unsigned char* raw = xs + bpr * kXColBytes;                 // raw activation inputs
+    unsigned char* ring = raw + a.raw_bytes;                    // kWaves x SLOTS slots
+    float* dots = reinterpret_cast<float*>(ring + kWaves * SLOTS * kSlotBytes);  // 64 per wave
+    float* red = dots + kWaves * 64;                            // kWaves floats
+    float* rowbuf = red + kWaves;                               // rows_per_wave per wave
+
+    // ---- 1. the activation inputs, this wave's share of 1 KiB pieces ------
+    const uint32_t raw_lds = lds_addr(raw);
+    if constexpr (XMODE == NB_X_BF16) {
+        const int nb = 2 * K;
+        for (int p = wave; p * 1024 < nb; p += kWaves)
+            dma_piece(raw_lds, static_cast<const uint8_t*>(a.x), nb, p, lane);
+    } else {
+        // x (fp32) at raw[0, 4K); the norm weights, or up (the second half
+        // of gate | up), at raw[sofs, sofs + 4K), sofs = 4K rounded up to
+        // whole pieces so that x's last piece cannot overwrite them
+        const int nb = 4 * K;
+        const uint8_t* xb = static_cast<const uint8_t*>(a.x);
+        const uint8_t* sb = XMODE == NB_X_RMSNORM ? reinterpret_cast<const uint8_t*>(a.norm_w)
+                                                  : xb + nb;
+        for (int p = wave; p * 1024 < nb; p += kWaves) {
+            dma_piece(raw_lds, xb, nb, p, lane);
+            dma_piece(raw_lds + a.raw_bytes / 2, sb, nb, p, lane);
+        }
+    }
+
+    // ---- 2. this wave's chunks and their first loads ------------------------
+    // The workgroup takes a contiguous run of units (a unit is `unit`
+    // consecutive chunks), dealt to its waves in turn: wave w takes units
+    // u0 + w, u0 + w + kWaves, ..., so the waves of a CU (and so its SIMDs)
+    // get equal shares to within one unit.
+    const int nunits = (a.nchunks + a.unit - 1) / a.unit;
+    const int u0 = (int)((int64_t)blockIdx.x * nunits / gridDim.x);
+    const int u1 = (int)((int64_t)(blockIdx.x + 1) * nunits / gridDim.x);
+    const int my_units = u1 - u0 > wave ? (u1 - u0 - wave + kWaves - 1) / kWaves : 0;
+    const int last_unit_chunks = a.nchunks - (nunits - 1) * a.unit;
+    // chunks of this wave: unit k = u0 + wave + k * kWaves holds chunks
+    // k_unit * unit .. (+ unit - 1), fewer in the problem's last unit
+    const int n_full = my_units * a.unit;
+    const bool has_last = my_units > 0 && u0 + wave + (my_units - 1) * kWaves == nunits - 1;
+    const int n = has_last ? n_full - a.unit + last_unit_chunks : n_full;
+    auto chunk_of = [&](int i) { return (u0 + wave + (i / a.unit) * kWaves) * a.unit + i % a.unit; };
+    unsigned char* my_ring = ring + wave * SLOTS * kSlotBytes;
+    const uint32_t ring_lds = lds_addr(my_ring);
+    const int64_t total_blocks = (int64_t)a.N * bpr;
+    const uint8_t* ilast = a.packed + total_blocks * 48 - 16;
+    const uint8_t* clast = reinterpret_cast<const uint8_t*>(a.codebook) + total_blocks * 32 - 16;
+    auto issue = [&](int c, int slot) {
+        const int64_t b0 = (int64_t)c * R * bpr;
+        const uint8_t* ip = a.packed + b0 * 48 + 16 * lane;
+        const uint8_t* cp = reinterpret_cast<const uint8_t*>(a.codebook) + b0 * 32 + 16 * lane;
+        const uint32_t dst = __builtin_amdgcn_readfirstlane(ring_lds + slot * kSlotBytes);
+        dma16<0>(dst, min(ip, ilast));
+        dma16<0>(dst + 1024, min(ip + 1024, ilast));
+        dma16<0>(dst + 2048, min(ip + 2048, ilast));
+        dma16<0>(dst + kSlotIdx, min(cp, clast));
+        dma16<0>(dst + kSlotIdx + 1024, min(cp + 1024, clast));
+    };
+    const int first = min(n, SLOTS);
+    for (int i = 0; i < first; ++i) issue(chunk_of(i), i);
+
+    // ---- 3. activations: wait for their pieces (the weights stay in flight),
+    //         form them in fp32, round to bf16, stage in the selector layout
+    wait_vm_n<SLOTS * kLoads>(first * kLoads);
+    __syncthreads();  // every wave's pieces are in LDS
+    const int ng = K >> 3;
+    constexpr int kMaxG = (kMaxK / 8 + kThreads - 1) / kThreads;
+    float norm = 1.f;
+    if constexpr (XMODE == NB_X_RMSNORM) {
+        const float* xf = reinterpret_cast<const float*>(raw);
+        float ss = 0.f;
+        for (int i = tid; i < K; i += kThreads) ss += xf[i] * xf[i];
+        ss = wsum(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float t = 0.f;
+        for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
+        norm = sqrtf(t / (float)K + a.eps);
+    }
+    uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
+#pragma unroll
+    for (int j = 0; j < kMaxG; ++j) {
+        const int g = tid + j * kThreads;
+        if (g < ng) {
+            uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                uint16_t v;
+                if constexpr (XMODE == NB_X_BF16) {
+                    v = reinterpret_cast<const uint16_t*>(raw)[8 * g + e];
+                } else {
+                    const float xv = reinterpret_cast<const float*>(raw)[8 * g + e];
+                    const float sv = reinterpret_cast<const float*>(raw + a.raw_bytes / 2)[8 * g + e];
+                    // RMSNorm.forward's (x / norm) * w, generate_torch.py:37; silu(g) * u,
+                    // 116-117 (exp(-g) by v_exp_f32, a few ulp, below the bf16 rounding)
+                    const float r = XMODE == NB_X_RMSNORM ? (xv / norm) * sv
+                                                          : (xv / (1.0f + __expf(-xv))) * sv;
+                    v = f32_to_bf16_rne(r);
+                }
+                col[staged_half(g & 15, e)] = v;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- 4. the wave's chunks: wait, read the slot, refill it, compute ------
+    float* wdots = dots + wave * 64;
+    float* wrows = rowbuf + wave * a.rows_per_wave;
+    const int row_in = lane / bpr;
+    const int col = lane - row_in * bpr;
+    for (int i = 0; i < n; ++i) {
+        const int slot = i % SLOTS;
+        const int c = chunk_of(i);
+        const int rows = min(R, a.N - c * R);
+        const int live = rows * bpr;
+        u32x4_t xv[16];   // the lane's 16 activation units
+        const unsigned char* xb = xs + (lane < live ? col : 0) * kXColBytes;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
+        const int issued = min(n, i + SLOTS);
+        wait_vm_n<(SLOTS - 1) * kLoads>((issued - i - 1) * kLoads);
+        const unsigned char* src = my_ring + slot * kSlotBytes;
+        const u32x4_t* pi = reinterpret_cast<const u32x4_t*>(src + 48 * lane);
+        const u32x4_t* pc = reinterpret_cast<const u32x4_t*>(src + kSlotIdx + 32 * lane);
+        const u32x4_t d0 = pi[0], d1 = pi[1], d2 = pi[2], e0 = pc[0], e1 = pc[1];
+        wait_lds();
+        if (i + SLOTS < n) issue(chunk_of(i + SLOTS), slot);
+        const f32x4_t acc = block_dot(d0, d1, d2, e0, e1, xv);
+        wdots[lane] = diag_of(acc, lane);
+        wait_lds();
+        // row sums: lane r < rows adds the bpr dot products of row r, 16
+        // independent loads at a time (one LDS latency per 16), in a fixed
+        // order; lanes past the rows read row 0 and store nothing
+        {
+            const float* p = wdots + (lane < rows ? lane : 0) * bpr;
+            float acc[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+            for (int j0 = 0; j0 < bpr; j0 += 16) {
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) v[q] = p[min(j0 + q, bpr - 1)];
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[q] += j0 + q < bpr ? v[q] : 0.f;
+            }
+#pragma unroll
+            for (int h = 8; h > 0; h >>= 1) {
+#pragma unroll
+                for (int q = 0; q < h; ++q) acc[q] += acc[q + h];
+            }
+            if (lane < rows) wrows[i * R + lane] = acc[0];
+        }
+        wait_lds();  // wdots is rewritten by the next chunk
+    }
+
+    // ---- 5. the wave's rows, written once, unit by unit --------------------
+    for (int k = 0; k * a.unit < n; ++k) {
+        const int c = chunk_of(k * a.unit);
+        const int row0 = c * R;
+        const int nrows = min(a.N, min(c + a.unit, a.nchunks) * R) - row0;
+        const float* ur = wrows + k * a.unit * R;
+        if (a.y_mode == NB_Y_SILU_PAIRS) {
+            // rows 2i, 2i+1 are gate row i and up row i (row0 and nrows are even)
+            bf16_bits* act = static_cast<bf16_bits*>(a.y) + row0 / 2;
+            for (int q = lane; q < nrows / 2; q += 64) {
+                const float g = ur[2 * q], u = ur[2 * q + 1];
+                act[q] = f32_to_bf16_rne((g / (1.0f + __expf(-g))) * u);
+            }
+        } else {
+            for (int r = lane; r < nrows; r += 64) {
+                const float v = ur[r];
+                const int row = row0 + r;
+                if (a.y_dtype == NB_BF16) {
+                    *as_global_mut(static_cast<bf16_bits*>(a.y) + row) = f32_to_bf16_rne(v);
+                } else if (a.y_mode == NB_Y_ADD) {
+                    float* yp = static_cast<float*>(a.y) + row;
+                    *as_global_mut(yp) = *as_global(yp) + v;   // the row is this wave's alone
+                } else {
+                    *as_global_mut(static_cast<float*>(a.y) + row) = v;
+                }
+            }
+        }
+    }
+}
+
+struct RowsShape {
+    int R, nchunks, unit, G, rows_per_wave, raw_bytes, slots;
+    size_t lds;
+};
+
+RowsShape rows_shape(const StreamProblem& p) {
+    RowsShape s;
+    const int bpr = p.K / 128;
+    s.R = 64 / bpr;
+    s.nchunks = (p.N + s.R - 1) / s.R;
+    // gate|up pairs must not be split between waves: with R odd, two chunks
+    // (an even number of rows) are the unit of the split
+    s.unit = (p.y_mode == NB_Y_SILU_PAIRS && (s.R & 1)) ? 2 : 1;
+    const int nunits = (s.nchunks + s.unit - 1) / s.unit;
+    s.G = std::max(1, std::min(device_cu_count(), (nunits + kWaves - 1) / kWaves));
+    const int per_wg = (nunits + s.G - 1) / s.G;   // the largest workgroup share
+    s.rows_per_wave = (per_wg + kWaves - 1) / kWaves * s.unit * s.R;
+    // bf16 x; or fp32 x and a second fp32 input, each from a whole piece
+    s.raw_bytes = p.x_mode == NB_X_BF16 ? (2 * p.K + 1023) / 1024 * 1024
+                                        : 2 * ((4 * p.K + 1023) / 1024 * 1024);
+    const size_t fixed = (size_t)bpr * kXColBytes + s.raw_bytes + (size_t)kWaves * 64 * 4 +
+                         (size_t)kWaves * 4 + (size_t)kWaves * s.rows_per_wave * 4;
+    s.slots = fixed + (size_t)kWaves * 3 * kSlotBytes <= (size_t)device_lds_bytes() ? 3 : 2;
+    s.lds = fixed + (size_t)kWaves * s.slots * kSlotBytes;
+    return s;
+}
+
+template <int XMODE>
+void launch_mode(const RowsShape& s, const RowsArgs& a, hipStream_t stream) {
+    if (s.slots == 3) {
+        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 3>), dim3(s.G), dim3(kThreads), s.lds,
+                           stream, a);
+    } else {
+        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 2>), dim3(s.G), dim3(kThreads), s.lds,
+                           stream, a);
+    }
+}
+
+}  // namespace
+
+bool gemv_rows_fits(const StreamProblem& p) {
+    if (p.K % 128 || p.K < 128 || p.K > kMaxK || p.N < 1) return false;
+    return rows_shape(p).lds <= (size_t)device_lds_bytes();
+}
+
+int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream) {
+    const RowsShape s = rows_shape(p);
+    RowsArgs a;
+    a.packed = p.packed;
+    a.codebook = p.codebook;
+    a.x = p.x;
+    a.norm_w = p.norm_w;
+    a.y = p.y;
+    a.N = p.N;
+    a.K = p.K;
+    a.bpr = p.K / 128;
+    a.R = s.R;
+    a.nchunks = s.nchunks;
+    a.unit = s.unit;
+    a.rows_per_wave = s.rows_per_wave;
+    a.raw_bytes = s.raw_bytes;
+    a.y_mode = p.y_mode;
+    a.y_dtype = y_dtype;
+    a.eps = p.eps;
+    switch (p.x_mode) {
+        case NB_X_BF16: launch_mode<NB_X_BF16>(s, a, stream); break;
+        case NB_X_RMSNORM: launch_mode<NB_X_RMSNORM>(s, a, stream); break;
+        default: launch_mode<NB_X_SILU_MUL>(s, a, stream); break;
+    }
+    return check_launch("nb_gemv_batched");
+}
+
+}  // namespace nb

@@ -560,6 +560,10 @@ static int aligned_at(const StreamProblem* hp, int nprob, int64_t c) {
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
                        int nprob, int y_dtype, hipStream_t stream) {
     if (nprob == 0) return NB_OK;
+    // a single problem (a decode step's launch) takes the whole-row kernel
+    if (nprob == 1 && gemv_rows_fits(host_probs[0])) {
+        return launch_gemv_rows(host_probs[0], y_dtype, stream);
+    }
     const StreamProblem& last = host_probs[nprob - 1];
     const int total = last.chunk_begin + last.nchunks;
     if (total == 0) return NB_OK;

@@ -85,6 +85,10 @@ int build_stream_table(const nb_batch_item* items, int count, StreamProblem* out
 
 // Launches the streaming kernel over the problem table (device copy for the
 // kernel, host copy to plan the workgroup ranges).
+// One problem per launch, whole-row chunks (nb_gemv_rows.hip): the launches
+// of a decode step.  gemv_rows_fits says whether its LDS holds the problem.
+bool gemv_rows_fits(const StreamProblem& p);
+int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream);
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
                        int nprob, int y_dtype, hipStream_t stream);
 

@@ -37,6 +37,20 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _interleave_rows(a, b):
+    """One packed layer whose rows alternate a's row i and b's row i (same
+    shape, K % 128 == 0 so a row is whole blocks): row 2i = a row i, row
+    2i + 1 = b row i."""
+    N, K = a.out_features, a.in_features
+    rb = K // 128
+    pa = a.packed_indices[: N * rb * 48].view(N, 1, rb * 48)
+    pb = b.packed_indices[: N * rb * 48].view(N, 1, rb * 48)
+    ca, cb = a.codebook.view(N, 1, rb, -1), b.codebook.view(N, 1, rb, -1)
+    packed = torch.cat([pa, pb], dim=1).reshape(-1).contiguous()
+    cbk = torch.cat([ca, cb], dim=1).reshape(2 * N * rb, -1).contiguous()
+    return packed, cbk
+
+
 def _fuse_rows(layers):
     """One packed layer holding the rows of several (same in_features, rows
     never share a block): streams and codebooks concatenated."""
@@ -49,6 +63,10 @@ class _DecoderBase:
     """Device-resident state shared by the decode engines: fused weights,
     norms, caches, embedding copies, the decode state, forced and chosen
     tokens, and the whole-sequence API."""
+
+    # row order of the fused gate|up layer: "stacked" (all gate rows, then
+    # all up rows) or "interleaved" (gate row i, up row i, ...)
+    _gu_rows = "stacked"
 
     def __init__(self, model: PackedGPT, max_steps: int | None = None):
         cfg = model.cfg
@@ -82,7 +100,10 @@ class _DecoderBase:
         self.norms = []
         for blk in model.blocks:
             qkv_p, qkv_c, _, _ = _fuse_rows([blk.attn.qkv])
-            gu_p, gu_c, _, _ = _fuse_rows([blk.ffn.gate, blk.ffn.up])
+            if self._gu_rows == "interleaved":
+                gu_p, gu_c = _interleave_rows(blk.ffn.gate, blk.ffn.up)
+            else:
+                gu_p, gu_c, _, _ = _fuse_rows([blk.ffn.gate, blk.ffn.up])
             o, dn = blk.attn.out_proj, blk.ffn.down
             self.fused.append(((qkv_p, qkv_c), (o.packed_indices, o.codebook), (gu_p, gu_c),
                                (dn.packed_indices, dn.codebook)))
@@ -166,6 +187,8 @@ class DecodeEngine(_DecoderBase):
     """Device-resident greedy decoder for one sequence (batch 1): one HIP
     graph of launches per token."""
 
+    _gu_rows = "interleaved"   # the gate|up GEMV hands silu(gate) * up to down
+
     def __init__(self, model: PackedGPT, max_steps: int | None = None,
                  record_layers: bool = False):
         """``record_layers``: after every layer the step also copies the
@@ -179,7 +202,7 @@ class DecodeEngine(_DecoderBase):
         self.h = z(C, dt=bf16)       # normalised embedding row (layer 0) and final norm
         self.qkv = z(3 * C)
         self.att = z(C, dt=bf16)
-        self.gu = z(2 * F)
+        self.act = z(F, dt=bf16)     # silu(gate) * up, the down projection's input
         self.work = z(int(_lib.load().nb_attention_work_floats(H)))
         self.done = z(H, dt=torch.int32)
         # Fused forms of the packed GEMVs (nb_batch_item x_mode / y_mode):
@@ -196,9 +219,9 @@ class DecodeEngine(_DecoderBase):
             self.gemvs.append((
                 ops.GemvBatch([qkv_item]),
                 ops.GemvBatch([(self.att, o_p, o_c, self.x, C, C, add)]),
-                ops.GemvBatch([(self.x, gu_p, gu_c, self.gu, 2 * F, C,
-                                {"x": ("rmsnorm", ln2, eps)})]),
-                ops.GemvBatch([(self.gu, d_p, d_c, self.x, C, F, {"x": "silu_mul", "y": "add"})]),
+                ops.GemvBatch([(self.x, gu_p, gu_c, self.act, 2 * F, C,
+                                {"x": ("rmsnorm", ln2, eps), "y": "silu_pairs"})]),
+                ops.GemvBatch([(self.act, d_p, d_c, self.x, C, F, add)]),
             ))
         self.graph = None
 
@@ -224,8 +247,8 @@ class DecodeEngine(_DecoderBase):
                                      _ptr(self.done), _ptr(self.att), BF, self.H, self.D,
                                      self.ctx, s))
             g_o.run()                        # x += W_o att
-            g_gu.run()                       # gu = W_gu rmsnorm(x)
-            g_d.run()                        # x += W_down (silu(gate) * up)
+            g_gu.run()                       # act = silu(gate) * up of rmsnorm(x)
+            g_d.run()                        # x += W_down act
             if self.layer_x is not None:
                 self.layer_x[l].copy_(self.x)
         ck(lib.nb_add_rmsnorm(_ptr(self.x), None, None, st, _ptr(self.ln_f), _ptr(self.h),

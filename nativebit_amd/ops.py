@@ -148,8 +148,10 @@ class GemvBatch:
       bf16((x / sqrt(mean(x^2) + eps)) * w), generate_torch.py:29-38) or
       "silu_mul" (x is the (2K,) float32 gate | up vector, the activations
       are bf16(silu(gate) * up), generate_torch.py:116-117);
-    * ``y``: "store" (default) or "add" (y += result, float32 y; the
-      residual add, generate_torch.py:128-132).
+    * ``y``: "store" (default), "add" (y += result, float32 y; the
+      residual add, generate_torch.py:128-132) or "silu_pairs" (rows
+      alternate gate and up: y is the (N/2,) bfloat16 vector
+      silu(gate) * up, generate_torch.py:116-117; one item per batch).
 
     ``m`` > 1 (up to 16) makes every item a skinny GEMM over m activation
     rows (nb_gemm_skinny_batched): x is an (m, K) bfloat16 matrix and y an
@@ -197,16 +199,24 @@ class GemvBatch:
                 shape = f"({m}, {x_n})" if m > 1 else f"({x_n},)"
                 raise TypeError(f"item {i}: x must be a contiguous {shape} {x_dt} tensor")
             yf = form.get("y", "store")
-            if yf not in ("store", "add"):
+            if yf not in ("store", "add", "silu_pairs"):
                 raise ValueError(f"item {i}: unknown output form {yf!r}")
-            y_mode = _lib.NB_Y_ADD if yf == "add" else _lib.NB_Y_STORE
+            y_mode = {"store": _lib.NB_Y_STORE, "add": _lib.NB_Y_ADD,
+                      "silu_pairs": _lib.NB_Y_SILU_PAIRS}[yf]
             if yf == "add" and y.dtype != torch.float32:
                 raise TypeError(f"item {i}: y += result needs a float32 y")
+            if yf == "silu_pairs":
+                if m != 1 or len(self.items) != 1:
+                    raise ValueError("the silu_pairs output form takes one item of one row")
+                if y.dtype != torch.bfloat16 or y.numel() * 2 != N or not y.is_contiguous():
+                    raise ValueError(f"item {i}: silu_pairs writes a contiguous ({N // 2},) "
+                                     "bfloat16 y")
             if packed.dtype != torch.uint8 or cb.dtype != torch.float32:
                 raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
             if cb.shape != (N * K // 128, 8) or packed.numel() < packed_nbytes(N * K, 3):
                 raise ValueError(f"item {i}: not a 3-bit / 8-entry / block-128 {N}x{K} layer")
-            if y.numel() != m * N or y.dtype not in _DT or not y.is_contiguous():
+            if yf != "silu_pairs" and (y.numel() != m * N or y.dtype not in _DT or
+                                       not y.is_contiguous()):
                 shape = f"({m}, {N})" if m > 1 else f"({N},)"
                 raise ValueError(f"item {i}: y must be a contiguous {shape} float32/bfloat16 tensor")
             if y_dt is None:

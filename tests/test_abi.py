@@ -180,7 +180,15 @@ def test_batch_fused_forms_validation():
     assert plan(*base, _lib.NB_X_SILU_MUL, 0, None, 0.0, 0) == _lib.NB_OK
     assert plan(*base, 3, 0, None, 0.0, 0) == _lib.NB_EINVAL           # unknown x_mode
     assert plan(*base, -1, 0, None, 0.0, 0) == _lib.NB_EINVAL
-    assert plan(*base, 0, 2, None, 0.0, 0) == _lib.NB_EINVAL           # unknown y_mode
+    assert plan(*base, 0, 3, None, 0.0, 0) == _lib.NB_EINVAL           # unknown y_mode
+    P2 = _lib.NB_Y_SILU_PAIRS
+    assert plan(*base, X, P2, FAKE, 1e-5, 0) == _lib.NB_OK             # gate|up pairs
+    assert plan(FAKE, FAKE, FAKE, FAKE, 33, 256, 0, P2, None, 0.0, 0) == _lib.NB_EINVAL  # odd N
+    two = (Item * 2)(Item(*base, 0, P2, None, 0.0, 0), Item(*base, 0, 0, None, 0.0, 0))
+    assert lib.nb_gemv_batch_plan(two, 2, ctypes.create_string_buffer(
+        lib.nb_gemv_batch_table_bytes(2)), lib.nb_gemv_batch_table_bytes(2)) == \
+        _lib.NB_EUNSUPPORTED                                            # pairs not alone
+    assert batched(_lib.NB_F32, *base, 0, P2, None, 0.0, 0) == _lib.NB_EUNSUPPORTED  # bf16 only
     assert plan(*base, X, 0, None, 1e-5, 0) == _lib.NB_EINVAL          # rmsnorm without weights
     assert plan(*base, X, 0, FAKE + 4, 1e-5, 0) == _lib.NB_EALIGN      # weights misaligned
     assert plan(*base, X, 0, FAKE, -1.0, 0) == _lib.NB_EINVAL          # negative eps

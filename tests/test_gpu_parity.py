@@ -540,6 +540,95 @@ def test_batched_fused_forms(dev):
         assert rel(y.cpu(), refs[i]) <= REL_F32, (i, rel(y.cpu(), refs[i]))
 
 
+@pytest.mark.parametrize("N,K", [(2560, 2560), (7680, 2560), (13824, 2560), (2560, 6912),
+                                 (1, 128), (5, 128), (1000, 384), (71, 8192), (333, 1280)])
+@pytest.mark.parametrize("mode,yf", [("bf16", "store"), ("rmsnorm", "store"), ("bf16", "add"),
+                                     ("silu_mul", "add"), ("rmsnorm", "add")])
+def test_single_item_rows_kernel(dev, N, K, mode, yf):
+    """A batch of one item runs the whole-row kernel (nb_gemv_rows.hip):
+    every activation form and output form, chunks of 64 / bpr rows with a
+    partial last chunk, K from one block to 64 blocks per row -- against
+    the fp64 brute force over the bf16 activations formed on the CPU, and
+    against the same item in a two-item batch (the 64-block-chunk kernel)."""
+    note(f"rows kernel {N}x{K} x={mode} y={yf}")
+    g = torch.Generator().manual_seed(N * 7 + K)
+    eps = 1e-6
+    idx, p, cb = random_layer(N, K, 3, 8, 128, N + K)
+    pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    form = {"y": yf}
+    if mode == "rmsnorm":
+        x = torch.randn(K, generator=g) * 3
+        w = 1 + 0.1 * torch.randn(K, generator=g)
+        form["x"] = ("rmsnorm", w.to(dev), eps)
+        a = _fused_activations(mode, x, w, eps)
+    elif mode == "silu_mul":
+        x = torch.randn(2 * K, generator=g) * 2
+        form["x"] = "silu_mul"
+        a = _fused_activations(mode, x)
+    else:
+        x = torch.randn(K, generator=g).to(torch.bfloat16)
+        a = x
+    y0 = torch.randn(N, generator=g) if yf == "add" else torch.zeros(N)
+    xd = x.to(dev)
+
+    def out():
+        return y0.clone().to(dev) if yf == "add" else torch.full((N,), float("nan"), device=dev)
+    y1, y2 = out(), out()
+    ops.GemvBatch([(xd, pt, ct, y1, N, K, form)]).run()
+    # the same item beside a one-row dummy item: the batched (64-block chunk) kernel
+    didx, dp, dcb = random_layer(1, 128, 3, 8, 128, 5)
+    dummy = (torch.zeros(128, dtype=torch.bfloat16, device=dev), torch.from_numpy(dp).to(dev),
+             torch.from_numpy(dcb).to(dev), torch.empty(1, device=dev), 1, 128)
+    ops.GemvBatch([(xd, pt, ct, y2, N, K, form), dummy]).run()
+    ref = ref_gemv(a, idx, cb, 128, N, K)[0] + y0.double().numpy()
+    assert np.isfinite(y1.cpu().numpy()).all()
+    assert rel(y1.cpu(), ref) <= REL_F32, rel(y1.cpu(), ref)
+    assert rel(y1.cpu(), y2.cpu()) <= 1e-3, rel(y1.cpu(), y2.cpu())
+
+
+@pytest.mark.parametrize("F,K", [(6912, 2560), (64, 128), (300, 384), (21, 2560)])
+def test_single_item_silu_pairs(dev, F, K):
+    """NB_Y_SILU_PAIRS: a gate|up layer whose rows alternate gate row i, up
+    row i writes act[i] = bf16(silu(gate_i . a) * (up_i . a)) -- the SwiGLU
+    product of generate_torch.py:116-117 -- equal to forming it on the CPU
+    from the fp64 brute-force rows (bf16 bar: 1e-2), and to the stacked
+    gate|up GEMV followed by the silu_mul activation form up to bf16
+    rounding of a few values."""
+    note(f"silu pairs F={F} K={K}")
+    g = torch.Generator().manual_seed(F + K)
+    eps = 1e-6
+    gi, gp, gcb = random_layer(F, K, 3, 8, 128, F)
+    ui, up, ucb = random_layer(F, K, 3, 8, 128, F + 1)
+    # interleave rows on the host: row 2i = gate i, row 2i+1 = up i
+    bpr = K // 128
+    gidx, uidx = gi.reshape(F, bpr * 128), ui.reshape(F, bpr * 128)
+    iidx = np.stack([gidx, uidx], axis=1).reshape(-1)
+    icb = np.stack([gcb.reshape(F, bpr, 8), ucb.reshape(F, bpr, 8)], axis=1).reshape(-1, 8)
+    ipk = torch.from_numpy(O.pack(iidx, 3)).to(dev)
+    icbt = torch.from_numpy(np.ascontiguousarray(icb)).to(dev)
+    x = torch.randn(K, generator=g) * 3
+    w = 1 + 0.1 * torch.randn(K, generator=g)
+    wd = w.to(dev)
+    act = torch.full((F,), float("nan"), dtype=torch.bfloat16, device=dev)
+    ops.GemvBatch([(x.to(dev), ipk, icbt, act, 2 * F, K,
+                    {"x": ("rmsnorm", wd, eps), "y": "silu_pairs"})]).run()
+    a = _fused_activations("rmsnorm", x, w, eps)
+    r = ref_gemv(a, iidx, icb, 128, 2 * F, K)[0]
+    gate, upv = torch.from_numpy(r[0::2]), torch.from_numpy(r[1::2])
+    ref = torch.nn.functional.silu(gate) * upv
+    got = act.float().cpu()
+    assert torch.isfinite(got).all()
+    assert rel(got, ref) <= REL_BF16, rel(got, ref)
+    # the unfused route: stacked gate|up rows (fp32 out), then silu(gate) * up
+    spk = torch.from_numpy(O.pack(np.concatenate([gi, ui]), 3)).to(dev)
+    scb = torch.from_numpy(np.concatenate([gcb, ucb])).to(dev)
+    gu = torch.empty(2 * F, device=dev)
+    ops.GemvBatch([(x.to(dev), spk, scb, gu, 2 * F, K, {"x": ("rmsnorm", wd, eps)})]).run()
+    gu = gu.cpu()
+    unfused = (torch.nn.functional.silu(gu[:F]) * gu[F:]).to(torch.bfloat16).float()
+    assert rel(got, unfused) <= 4e-3, rel(got, unfused)
+
+
 def test_batched_many_small_fused_items(dev):
     """Many small items, so one workgroup forms several problems'
     activations (each RMSNorm with its own barriers) and takes chunks of
