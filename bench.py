@@ -395,7 +395,13 @@ PREFILL_SHAPES = (("qkv", 7680, 2560), ("o", 2560, 2560), ("gate|up", 13824, 256
 
 
 def bench_prefill(dev, random_weights=False):
-    """Config 4a: prefill-sized contraction with the packed weights."""
+    """Config 4a: prefill-sized contraction with the packed weights.
+
+    The value is nb_gemm_prefill: the hand-written MFMA kernels that
+    dequantize the 3-bit stream into LDS tiles.  Beside it, for comparison
+    only: nb_gemm_prefill_ws (the weight expanded to bf16 in a workspace,
+    then hipBLASLt) and torch's dense bf16 matmul of an already-unpacked
+    weight."""
     from nativebit_amd import ops, synth
     layers = {n: _make(random_weights)(N, K, seed=50 + i, device=dev)
               for i, (n, N, K) in enumerate(PREFILL_SHAPES)}
@@ -403,21 +409,22 @@ def bench_prefill(dev, random_weights=False):
     for M in (512, 2048):
         xs = {K: synth.make_activation(K, m=M, seed=M + K, device=dev, dtype=torch.bfloat16)
               for K in (2560, 6912)}
-        per, tot_ms, tot_fl, ref_ms, fused_ms = {}, 0.0, 0, 0.0, 0.0
+        per, tot_ms, tot_fl, ref_ms, blas_ms = {}, 0.0, 0, 0.0, 0.0
         for n, N, K in PREFILL_SHAPES:
             lay = layers[n]
             y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-            ms = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y), 20)
-            ms_fused = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K,
-                                                           out=y, path="fused"), 20)
+            ms = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y),
+                            20)
+            ms_blas = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K,
+                                                          out=y, path="blas"), 20)
             w = torch.empty(N, K, dtype=torch.bfloat16, device=dev).normal_()
             ms_ref = event_time(lambda: torch.matmul(xs[K], w.T), 20)
             fl = 2 * M * N * K
             per[n] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / ms / 1e9, 1),
-                      "fused_kernel_us": round(ms_fused * 1e3, 1),
+                      "blas_workspace_us": round(ms_blas * 1e3, 1),
                       "torch_dense_bf16_us": round(ms_ref * 1e3, 1)}
-            fused_ms = fused_ms + ms_fused
             tot_ms += ms
+            blas_ms += ms_blas
             ref_ms += ms_ref
             tot_fl += fl
             del w
@@ -425,17 +432,16 @@ def bench_prefill(dev, random_weights=False):
                         "TFLOP_s": round(tot_fl / tot_ms / 1e9, 1),
                         "pct_bf16_mfma_peak": round(tot_fl / tot_ms / 1e9 / 2500 * 100, 2),
                         "model_26_layers_ms": round(26 * tot_ms, 3),
-                        "paths": {n: "blas" if ops.prefill_uses_blas(M, N, K) else "fused"
-                                  for n, N, K in PREFILL_SHAPES},
-                        "fused_kernel_layer_us": round(fused_ms * 1e3, 1),
+                        "blas_workspace_layer_us": round(blas_ms * 1e3, 1),
                         "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
                         "per_matmul": per}
-    out["note"] = ("us / TFLOP_s: ops.gemm_prefill's default path per shape ('paths': blas = "
-                   "nb_gemm_prefill_ws, W expanded to bf16 in a workspace by the format kernel, "
-                   "then one hipBLASLt GEMM, the expansion inside the timed call); "
-                   "fused_kernel: nb_gemm_prefill, whose MFMA kernel reads the 3-bit stream and "
-                   "codebooks directly; torch_dense_bf16 is torch.matmul on an already-unpacked "
-                   "bf16 weight (the reference's path also unpacks and gathers W on every call, "
+    out["note"] = ("us / TFLOP_s: nb_gemm_prefill, the hand-written MFMA kernels that read the "
+                   "3-bit stream and codebooks and dequantize into LDS (bf16 operands, fp32 "
+                   "accumulation, bf16 y); comparison columns only: blas_workspace = "
+                   "nb_gemm_prefill_ws (W expanded to bf16 in a workspace by the format kernel, "
+                   "then one hipBLASLt GEMM, the expansion inside the timed call), "
+                   "torch_dense_bf16 = torch.matmul on an already-unpacked bf16 weight (the "
+                   "reference's path also unpacks and gathers W on every call, "
                    "triton_kernel.py:258-275)")
     return out
 

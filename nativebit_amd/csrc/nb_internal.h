@@ -120,6 +120,10 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
 int launch_prefill(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
 
+// The same contraction with 256-output x 256/128-token tiles (nb_prefill2.hip).
+int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
+
 // hipBLASLt's own share of the prefill workspace, after the bf16 weight.
 constexpr int64_t kPrefillBlasWorkspace = 32ll << 20;
 

@@ -1,0 +1,332 @@
+// Prefill contraction with a packed weight, large tiles (gfx950).
+//
+//   Y[m][n] = sum_k X[m][k] * bf16(W[n][k]),   W 3-bit / 8-entry / block-128
+//
+// The reference computes this as unpack + gather + a dense matmul that
+// materialises W on every call (inference/triton_kernel.py:258-275; in bf16,
+// inference/eval_ppl.py:149-174).  Here a 512-thread workgroup owns a BN x
+// BM tile of Y^T (BN outputs x BM tokens) and walks K in steps of 64:
+//
+//   * the X slice (BM tokens x 64 bf16) arrives by global_load_lds_dwordx4
+//     (eight rows per instruction), 16-byte chunk c of row r in LDS slot
+//     c ^ (r & 7), so that eight consecutive rows read one chunk from eight
+//     different bank groups;
+//   * the W slice (BN rows x 64 weights: 24 index bytes per row, the codebook
+//     of the row's block) is loaded into registers two steps ahead; each
+//     thread turns half a row (32 indices) into bf16 with v_perm_b32 lookups
+//     into the block's codebook byte planes and stores it with the same
+//     swizzle;
+//   * eight waves (2 x 4) each own a (BN/4) x (BM/2) sub-tile of 16 x 16
+//     v_mfma_f32_16x16x32_bf16 tiles with W as the A operand and X as B, so
+//     a lane's accumulator holds four consecutive outputs n of one token m
+//     and the epilogue stores them as one vector;
+//   * two LDS stages and one barrier per step: while a step's MFMAs run, the
+//     next step's X slice is in flight and its W slice is dequantized, and
+//     the two waves of each SIMD overlap one's MFMAs with the other's
+//     dequantization and LDS reads.
+// Weights are the codebook entries rounded to bf16 (RNE), as the bf16 path;
+// accumulation is fp32.
+#include <algorithm>
+#include <type_traits>
+
+#include "nb_device.h"
+#include "nb_internal.h"
+
+namespace nb {
+namespace {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+
+// waves per workgroup: 8 (two per SIMD) or 4 (one per SIMD, 128 x 128 per wave)
+#ifndef NB_PREFILL_WAVES
+#define NB_PREFILL_WAVES 8
+#endif
+constexpr int kBK = 64;            // K per step: half a codebook block
+constexpr int kRowBytes = kBK * 2; // bf16 bytes of one row of a slice
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+    bf16x2_t v;
+    v.x = (__bf16)lo;
+    v.y = (__bf16)hi;
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// 8 bf16 weights (natural order) of one 24-bit index group from the byte
+// planes of the block's codebook: two selectors of four 3-bit indices, four
+// v_perm_b32 lookups, two interleaves per bf16 pair.
+__device__ __forceinline__ u32x4_t lookup8(uint32_t g, uint32_t lo0, uint32_t lo1, uint32_t hi0,
+                                           uint32_t hi1) {
+    const uint32_t h = (g & 0xfffu) | ((g << 4) & 0x0fff0000u);  // i0-3 low half, i4-7 high
+    const uint32_t sa = (h & 0x00070007u) | ((h << 5) & 0x07000700u);          // i0 i1 i4 i5
+    const uint32_t sb = ((h >> 6) & 0x00070007u) | ((h >> 1) & 0x07000700u);   // i2 i3 i6 i7
+    const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sa);
+    const uint32_t ha = __builtin_amdgcn_perm(hi1, hi0, sa);
+    const uint32_t lb = __builtin_amdgcn_perm(lo1, lo0, sb);
+    const uint32_t hb = __builtin_amdgcn_perm(hi1, hi0, sb);
+    u32x4_t w;
+    w.x = __builtin_amdgcn_perm(ha, la, 0x05010400u);  // i0 i1
+    w.y = __builtin_amdgcn_perm(hb, lb, 0x05010400u);  // i2 i3
+    w.z = __builtin_amdgcn_perm(ha, la, 0x07030602u);  // i4 i5
+    w.w = __builtin_amdgcn_perm(hb, lb, 0x07030602u);  // i6 i7
+    return w;
+}
+
+// LDS byte offset of 16-byte chunk c (0..7) of slice row r.
+__device__ __forceinline__ uint32_t swz(int r, int c) {
+    return (uint32_t)(r * kRowBytes + ((c ^ (r & 7)) << 4));
+}
+
+__device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(lds), "v"(src)
+                 : "memory", "m0");
+}
+
+template <typename T>
+__device__ __forceinline__ uint32_t lds_addr(T* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) T*)p;
+}
+
+struct Prefill2Args {
+    const uint16_t* x;
+    int64_t ldx;
+    const uint8_t* packed;
+    const float* codebook;
+    void* y;
+    int64_t ldy;
+    int y_dtype;
+    int M, N, K;
+};
+
+// One thread's share of a W slice: 12 index bytes (32 weights) per half
+// row it takes (H = 1 or 2) and the codebook of the row's block.  Each
+// 12-byte piece is one register tuple, so its loads land in place without
+// copies.
+template <int H>
+struct WRegs {
+    u32x4_t d[H];  // x, y, z of d[h]: the index bytes of half h
+    u32x4_t c0, c1;
+};
+
+template <int BM, int BN, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
+    constexpr int kThreads = 64 * WAVES;
+    constexpr int WGM = WAVES >= 16 ? 4 : 2;  // waves along the tokens
+    constexpr int WGN = WAVES / WGM;     // waves along the outputs
+    constexpr int WN = BN / WGN;         // outputs per wave (A operand rows)
+    constexpr int WM = BM / WGM;         // tokens per wave (B operand rows)
+    constexpr int TI = WN / 16, TJ = WM / 16;
+    constexpr int kXBytes = BM * kRowBytes, kWBytes = BN * kRowBytes;
+    constexpr int kStage = kXBytes + kWBytes;
+    constexpr int kXLoads = BM / (8 * WAVES);  // dma16 per wave per step (8 rows each)
+    // threads per W row: 2 (half a row each) or 1; with more threads than
+    // two per row, the first 2 BN threads dequantize
+    constexpr int TPR = kThreads >= 2 * BN ? 2 : kThreads / BN;
+    constexpr int H = 2 / TPR;           // 32-weight halves per thread
+    constexpr bool kAllDeq = kThreads <= 2 * BN;
+    static_assert(TPR == 1 || TPR == 2, "one or two threads per W row");
+    using WR = WRegs<H>;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int bpr = a.K / 128;
+    const int nsteps = a.K / kBK;
+    const uint32_t base = lds_addr(smem);
+
+    // X slice: instruction i of wave w covers slice rows 8 (kXLoads w + i)
+    // .. +7; lane l fills slot l & 7 of row 8 (...) + (l >> 3)
+    auto load_x = [&](int step, int stage) {
+#pragma unroll
+        for (int i = 0; i < kXLoads; ++i) {
+            const int r0 = (wave * kXLoads + i) * 8;
+            const int r = r0 + (lane >> 3);
+            const int c = (lane & 7) ^ (r & 7);
+            const int gm = min(m0 + r, a.M - 1);
+            const uint16_t* src = a.x + (int64_t)gm * a.ldx + (int64_t)step * kBK + c * 8;
+            dma16(__builtin_amdgcn_readfirstlane(base + stage * kStage + r0 * kRowBytes), src);
+        }
+    };
+    // W slice: thread t takes halves h0 .. h0 + H - 1 of row t / TPR
+    const int wr = (tid / TPR) % BN, h0 = (tid % TPR) * H;
+    const int gn = min(n0 + wr, a.N - 1);
+    const bool deq = kAllDeq || tid < 2 * BN;
+    auto load_w = [&](int step, WR& w) {
+        if (!deq) return;
+        const int64_t blk = (int64_t)gn * bpr + (step >> 1);
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const uint32_t* ip = reinterpret_cast<const uint32_t*>(
+                a.packed + blk * 48 + (step & 1) * 24 + (h0 + h) * 12);
+            w.d[h].x = ip[0];
+            w.d[h].y = ip[1];
+            w.d[h].z = ip[2];
+        }
+        const u32x4_t* cp = reinterpret_cast<const u32x4_t*>(a.codebook + blk * 8);
+        w.c0 = cp[0];
+        w.c1 = cp[1];
+    };
+    auto store_w = [&](int stage, const WR& w) {
+        if (!deq) return;
+        const uint32_t q0 = pack_bf16x2(__uint_as_float(w.c0.x), __uint_as_float(w.c0.y));
+        const uint32_t q1 = pack_bf16x2(__uint_as_float(w.c0.z), __uint_as_float(w.c0.w));
+        const uint32_t q2 = pack_bf16x2(__uint_as_float(w.c1.x), __uint_as_float(w.c1.y));
+        const uint32_t q3 = pack_bf16x2(__uint_as_float(w.c1.z), __uint_as_float(w.c1.w));
+        const uint32_t lo0 = __builtin_amdgcn_perm(q1, q0, 0x06040200u);
+        const uint32_t hi0 = __builtin_amdgcn_perm(q1, q0, 0x07050301u);
+        const uint32_t lo1 = __builtin_amdgcn_perm(q3, q2, 0x06040200u);
+        const uint32_t hi1 = __builtin_amdgcn_perm(q3, q2, 0x07050301u);
+        unsigned char* wt = smem + stage * kStage + kXBytes;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            // the four 24-bit groups of the half's 96 index bits
+            const u32x4_t d = w.d[h];
+            const uint32_t g[4] = {d.x & 0xffffffu, __builtin_amdgcn_alignbit(d.y, d.x, 24),
+                                   __builtin_amdgcn_alignbit(d.z, d.y, 16), d.z >> 8};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                *reinterpret_cast<u32x4_t*>(wt + swz(wr, (h0 + h) * 4 + j)) =
+                    lookup8(g[j], lo0, lo1, hi0, hi1);
+            }
+        }
+    };
+
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int fr = lane & 15, fq = lane >> 4;
+    f32x4_t acc[TI][TJ];
+#pragma unroll
+    for (int i = 0; i < TI; ++i)
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    WR wq0, wq1;  // W slices of even / odd steps (named, so they stay in registers)
+    load_x(0, 0);
+    load_w(0, wq0);
+    if (nsteps > 1) load_w(1, wq1);
+    store_w(0, wq0);
+    asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+    __syncthreads();
+
+    // One step on LDS stage CUR (= step & 1): the W slice of step + 2 goes
+    // into the registers this step's came from (already in LDS) and the next
+    // X slice is requested, the MFMAs run, then the next step's W slice
+    // (loaded one step ago) is dequantized into the other stage.
+    auto run_step = [&](int step, auto cur_c, WR& mine, WR& next) {
+        constexpr int cur = decltype(cur_c)::value;
+        // The next step's W slice was loaded a step ago and the previous
+        // step ended with vmcnt(0): passing its registers through an empty
+        // asm statement here puts the compiler's wait for them at this point
+        // (where it costs nothing), so the dequantization below may sit
+        // among the MFMAs without a wait that would also drain the X slice
+        // requested next (the compiler cannot see that load).
+#pragma unroll
+        for (int h = 0; h < H; ++h) asm volatile("" : "+v"(next.d[h]));
+        asm volatile("" : "+v"(next.c0), "+v"(next.c1));
+        if (step + 2 < nsteps) load_w(step + 2, mine);
+        if (step + 1 < nsteps) load_x(step + 1, cur ^ 1);
+        const unsigned char* xt = smem + cur * kStage;
+        const unsigned char* wt = xt + kXBytes;
+        auto mfma_k32 = [&](int ks) {  // 32 of the step's 64 K
+            const int c = ks * 4 + fq;
+            u32x4_t av[TI], bv[TJ];
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+                av[i] = *reinterpret_cast<const u32x4_t*>(wt + swz(wn * WN + i * 16 + fr, c));
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+                bv[j] = *reinterpret_cast<const u32x4_t*>(xt + swz(wm * WM + j * 16 + fr, c));
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8_t, av[i]), __builtin_bit_cast(bf16x8_t, bv[j]),
+                        acc[i][j], 0, 0, 0);
+        };
+        mfma_k32(0);
+        if (step + 1 < nsteps) store_w(cur ^ 1, next);
+        mfma_k32(1);
+        // the next X slice (direct-to-LDS, not tracked by the compiler) must
+        // be in LDS before the barrier; the W loads of step + 2, issued
+        // before it, have had the whole step to arrive
+        asm volatile("s_waitcnt vmcnt(0)" : : : "memory");
+        __syncthreads();
+    };
+    for (int step = 0; step < nsteps; step += 2) {
+        run_step(step, std::integral_constant<int, 0>{}, wq0, wq1);
+        if (step + 1 < nsteps) run_step(step + 1, std::integral_constant<int, 1>{}, wq1, wq0);
+    }
+
+    // D fragment (i, j): lane holds outputs n = 4 fq .. 4 fq + 3 of A sub-tile
+    // i for token fr of B sub-tile j
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int n = n0 + wn * WN + i * 16 + fq * 4;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int m = m0 + wm * WM + j * 16 + fr;
+            if (m >= a.M) continue;
+            const f32x4_t v = acc[i][j];
+            if (a.y_dtype == NB_BF16) {
+                bf16_bits* yp = static_cast<bf16_bits*>(a.y) + (int64_t)m * a.ldy + n;
+                if (n + 3 < a.N && ((a.ldy | n) & 3) == 0) {
+                    u32x2_t p;
+                    p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+                    p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+                    *reinterpret_cast<u32x2_t*>(yp) = p;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) yp[e] = f32_to_bf16_rne(v[e]);
+                }
+            } else {
+                float* yp = static_cast<float*>(a.y) + (int64_t)m * a.ldy + n;
+                if (n + 3 < a.N && ((a.ldy | n) & 3) == 0) {
+                    *reinterpret_cast<f32x4_t*>(yp) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) yp[e] = v[e];
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+    Prefill2Args a;
+    a.x = static_cast<const uint16_t*>(x);
+    a.ldx = ldx;
+    a.packed = packed;
+    a.codebook = codebook;
+    a.y = y;
+    a.ldy = ldy;
+    a.y_dtype = y_dtype;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    constexpr int BN = 256;
+    constexpr int W = NB_PREFILL_WAVES;
+    const int gn = (N + BN - 1) / BN;
+    // 256-token tiles when they give the CUs enough workgroups, else 128
+    const int cus = device_cu_count();
+    if ((int64_t)gn * ((M + 255) / 256) >= (int64_t)cus * 3 / 4) {
+        const size_t lds = 2 * (256 + BN) * kRowBytes;
+        hipLaunchKernelGGL((prefill2_kernel<256, BN, W>), dim3(gn, (M + 255) / 256),
+                           dim3(64 * W), lds, stream, a);
+    } else {
+        const size_t lds = 2 * (128 + BN) * kRowBytes;
+        hipLaunchKernelGGL((prefill2_kernel<128, BN, W>), dim3(gn, (M + 127) / 128),
+                           dim3(64 * W), lds, stream, a);
+    }
+    return check_launch("nb_gemm_prefill");
+}
+
+}  // namespace nb

@@ -21,10 +21,18 @@ from . import ops
 from .linear import BS, NE, PackedLinear  # noqa: F401
 
 
+def _as_gemv_input(x: torch.Tensor) -> torch.Tensor:
+    """x as the kernels take it: fp32 or bf16 as given, any other float type
+    cast to fp32 on the device (the reference's kernels load x as fp32,
+    triton_kernel.py:46, 174)."""
+    x = x.reshape(-1)
+    return x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
+
+
 def dequant_matvec_3bit(x: torch.Tensor, packed_indices: torch.Tensor,
                         codebook: torch.Tensor, N: int, K: int, tile_n=None) -> torch.Tensor:
     """y = W @ x for a 3-bit packed W (N x K), block 128; x (K,) -> y (N,) fp32."""
-    return ops.gemv(x.reshape(-1), packed_indices.reshape(-1), codebook.reshape(-1, NE),
+    return ops.gemv(_as_gemv_input(x), packed_indices.reshape(-1), codebook.reshape(-1, NE),
                     int(N), int(K), bits=3, block_size=BS)
 
 
@@ -43,7 +51,7 @@ def dequant_matvec(x: torch.Tensor, indices: torch.Tensor, codebook: torch.Tenso
     idx = indices.reshape(-1)
     if idx.dtype != torch.uint8:
         idx = idx.to(torch.uint8)
-    return ops.gemv(x.reshape(-1), idx.contiguous(), codebook.reshape(-1, codebook.shape[-1]),
+    return ops.gemv(_as_gemv_input(x), idx.contiguous(), codebook.reshape(-1, codebook.shape[-1]),
                     int(N), int(K), bits=8, block_size=BS)
 
 

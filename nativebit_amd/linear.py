@@ -7,10 +7,12 @@ float32), the same ``out_features`` / ``in_features`` attributes, the same
 a ``forward`` that takes any leading dimensions and returns float32 by
 default.  Differences, all deliberate:
 
-* every row count runs on the gfx950 kernels of libnativebit_amd.so (the
-  reference uses a CUDA kernel for one row and torch unpack+gather+matmul for
-  more); nothing falls back silently -- a failure raises NativeBitError
-  (the reference swallows every exception, triton_kernel.py:252);
+* up to 16 rows run the fused dequant-GEMV kernels; more rows of bf16
+  activations run the packed MFMA prefill kernels, and other batched inputs
+  (fp32 x, other formats) gather W on the device with the format kernel and
+  multiply it densely, as the reference's batched branch does; nothing falls
+  back silently -- a failure raises NativeBitError (the reference swallows
+  every exception, triton_kernel.py:252);
 * bit width, entries per block and block size are attributes (defaults 3, 8
   and 128, the reference's constants, triton_kernel.py:18-19);
 * ``out_dtype`` may be bfloat16 for callers that keep activations in bf16.
@@ -49,10 +51,17 @@ class PackedLinear(torch.nn.Module):
             raise ValueError(f"codebook has {codebook.shape[0]} blocks; "
                              f"{self.out_features}x{self.in_features} at block "
                              f"{self.block_size} needs {need_blocks}")
+        # the kernels read the stream of every (zero-padded) block
         need = ops.packed_nbytes(need_blocks * self.block_size, self.bits)
-        if packed_indices.numel() < ops.packed_nbytes(total, self.bits):
+        if packed_indices.numel() < need:
             raise ValueError(f"packed_indices has {packed_indices.numel()} bytes, "
-                             f"expected {need}")
+                             f"{need} needed")
+
+    def _standard(self) -> bool:
+        """The format of the MFMA prefill kernels: 3-bit, 8 entries, blocks of
+        128 along whole rows."""
+        return (self.bits == 3 and self.n_entries == NE and self.block_size == BS
+                and self.in_features % BS == 0)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         shape = x.shape
@@ -60,16 +69,27 @@ class PackedLinear(torch.nn.Module):
             raise ValueError(f"x last dim must be {self.in_features}, got {tuple(shape)}")
         x_flat = x.reshape(-1, self.in_features)
         if x_flat.dtype not in (torch.float32, torch.bfloat16):
+            # any other float type is read as fp32, as the reference's kernels
+            # load x (.to(tl.float32), triton_kernel.py:46, 174)
             x_flat = x_flat.to(torch.float32)
         M = x_flat.shape[0]
-        y = torch.empty((M, self.out_features), dtype=self.out_dtype, device=x.device)
-        for m0 in range(0, M, MAX_GEMV_ROWS):
-            m1 = min(M, m0 + MAX_GEMV_ROWS)
-            ops.gemv(x_flat[m0:m1], self.packed_indices, self.codebook,
-                     self.out_features, self.in_features, bits=self.bits,
-                     block_size=self.block_size, out_dtype=self.out_dtype,
-                     out=y[m0:m1])
-        return y.reshape(*shape[:-1], self.out_features)
+        N, K = self.out_features, self.in_features
+        if M <= MAX_GEMV_ROWS:
+            y = ops.gemv(x_flat, self.packed_indices, self.codebook, N, K, bits=self.bits,
+                         block_size=self.block_size, out_dtype=self.out_dtype)
+        elif x_flat.dtype == torch.bfloat16 and self._standard():
+            # the bf16 batched form (eval_ppl.py:149-174): the packed MFMA kernels
+            y = ops.gemm_prefill(x_flat, self.packed_indices, self.codebook, N, K,
+                                 out_dtype=self.out_dtype)
+        else:
+            # the reference's batched branch as it computes it (triton_kernel.py:
+            # 258-275): W gathered on the device at x's precision by the format
+            # kernel (exact fp32 copies of the codebook entries, or their bf16
+            # rounding), then one dense GEMM
+            w = ops.dequant(self.packed_indices, self.codebook, N * K, self.bits,
+                            self.block_size, x_flat.dtype).view(N, K)
+            y = (x_flat @ w.T).to(self.out_dtype)
+        return y.reshape(*shape[:-1], N)
 
     @staticmethod
     def from_packed(indices_np, codebook_np, weight_shape, device="cuda",

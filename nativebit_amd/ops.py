@@ -247,26 +247,16 @@ class GemvBatch:
                                                   self.m, _DT[self.y_dtype], stream))
 
 
-def prefill_uses_blas(M: int, N: int, K: int) -> bool:
-    """gemm_prefill's "auto" choice, from per-shape timings of both paths on
-    MI355X (M = 64..2048 on the 2.2B shapes): the workspace path wins for
-    long rows (K > 4096: the fused kernel has too few output tiles), small
-    matrices (N*K <= 8M: the bf16 expansion is cheap) and many rows; the
-    fused kernel wins for the wide K = 2560 shapes at a few hundred rows."""
-    if K > 4096 or N * K <= (8 << 20) or M >= 1024:
-        return True
-    return M >= 384 and N >= 10000
-
-
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
                  K: int, out_dtype: torch.dtype = torch.bfloat16,
                  out: torch.Tensor | None = None, path: str = "auto") -> torch.Tensor:
     """y = x @ bf16(W).T for a 3-bit / 8-entry / block-128 packed W (N x K);
     x (M, K) bfloat16, row-contiguous, fp32 accumulation.
 
-    ``path``: "fused" (nb_gemm_prefill: dequantization inside the MFMA
-    kernel), "blas" (nb_gemm_prefill_ws: W expanded to bf16 in a workspace,
-    then one hipBLASLt GEMM) or "auto" (prefill_uses_blas)."""
+    ``path``: "fused" or "auto" (nb_gemm_prefill: the packed weight is
+    dequantized into LDS inside the hand-written MFMA kernels), or "blas"
+    (nb_gemm_prefill_ws: W expanded to bf16 in a workspace, then one
+    hipBLASLt GEMM -- kept as a comparison)."""
     for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
         _require_cuda(name, t)
     _same_device(x, packed, codebook)
@@ -286,7 +276,7 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
     if path not in ("auto", "fused", "blas"):
         raise ValueError(f"unknown prefill path {path!r}")
     lib = _lib.load()
-    if path == "blas" or (path == "auto" and prefill_uses_blas(M, N, K)):
+    if path == "blas":
         nbytes = int(lib.nb_gemm_prefill_ws_bytes(M, N, K))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
         _lib.check(lib.nb_gemm_prefill_ws(

@@ -352,14 +352,32 @@ def test_packed_linear_api(dev):
     layer = PackedLinear.from_packed(idx.reshape(-1, 128), cb, (N, K), device=dev)
     assert torch.equal(layer.packed_indices.cpu(), torch.from_numpy(p))
     assert layer.out_features == N and layer.in_features == K
-    for xdt in (torch.float32, torch.bfloat16):
-        for shape in [(K,), (1, K), (1, 1, K), (3, K), (2, 5, K), (40, K)]:
+    # up to 16 rows: the GEMV kernels; more: the MFMA prefill kernels (bf16 x)
+    # or the device gather + dense GEMM (fp32 x, the reference's batched branch)
+    for xdt in (torch.float32, torch.bfloat16, torch.float16):
+        for shape in [(K,), (1, K), (1, 1, K), (3, K), (2, 5, K), (40, K), (300, K),
+                      (4, 100, K)]:
             note(f"PackedLinear x{shape} {xdt}")
             x = torch.randn(*shape, generator=torch.Generator().manual_seed(len(shape))).to(xdt)
             y = layer(x.to(dev))
             assert y.dtype == torch.float32 and y.shape == (*shape[:-1], N)
-            ref = ref_gemv(x.reshape(-1, K), idx, cb, 128, N, K)
+            # fp16 x is read as fp32 (the reference's kernels load x as fp32)
+            xr = x.float() if xdt == torch.float16 else x
+            ref = ref_gemv(xr.reshape(-1, K), idx, cb, 128, N, K)
             assert rel(y.cpu().reshape(-1, N), ref) <= REL_F32
+
+
+def test_packed_linear_other_format_batched(dev):
+    """A 4-bit / 16-entry / block-64 layer with many rows: the device gather
+    and a dense fp32 GEMM, equal to the fp64 brute force."""
+    N, K, M = 300, 640, 70
+    idx, p, cb = random_layer(N, K, 4, 16, 64, 41)
+    layer = PackedLinear(torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K,
+                         block_size=64)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(3))
+    y = layer(x.to(dev))
+    ref = O.matmul_f64(x.numpy(), O.dequant(idx, cb, 64, N * K).reshape(N, K))
+    assert rel(y.cpu(), ref) <= REL_F32
 
 
 def test_kernels_mirror(dev):
@@ -371,6 +389,11 @@ def test_kernels_mirror(dev):
     for fn in (kernels.dequant_matvec_3bit, kernels.dequant_matvec_3bit_cuda):
         y = fn(x.to(dev), pt, ct, N, K)
         assert y.shape == (N,) and rel(y.cpu(), ref) <= REL_F32
+    # fp16 x is read as fp32, as the reference's Triton kernels do
+    x16 = x.to(torch.float16)
+    ref16 = O.matmul_f64(x16.float().numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
+    y16 = kernels.dequant_matvec_3bit(x16.to(dev), pt, ct, N, K)
+    assert y16.dtype == torch.float32 and rel(y16.cpu(), ref16) <= REL_F32
     y8 = kernels.dequant_matvec(x.to(dev), torch.from_numpy(idx.reshape(-1, 128)).to(dev), ct, N, K)
     assert rel(y8.cpu(), ref) <= REL_F32
     assert torch.equal(kernels.pack_indices_to_3bit(torch.from_numpy(idx).to(dev)).cpu(),
