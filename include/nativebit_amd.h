@@ -357,6 +357,54 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
                       int V, int C, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Batched forward pass over T tokens (a prompt fed as one sequence, as
+ * PackedGPT.forward does with T > 1, inference/generate_torch.py:299-302):
+ * the non-matmul kernels; the packed matmuls are nb_gemm_prefill.  Rows are
+ * contiguous (row stride = width).  The caches are those of the decode
+ * step (keys [n_head][head_dim][ctx], values [n_head][ctx][head_dim], fp32).
+ * ------------------------------------------------------------------------ */
+/*
+ * Per row t < T: with emb and tokens, x[t] = emb[tokens[t]] (the embedding
+ * lookup); with add, x[t] += add[t] (a residual add); then h[t] =
+ * (x[t] / sqrt(mean(x[t]^2) + eps)) * w (C wide; x, add, emb, w fp32; h
+ * NB_F32 or NB_BF16).  x is updated in place.
+ * Replaces: RMSNorm.forward over a sequence (inference/generate_torch.py:
+ *           29-38) with the residual adds of TransformerBlock.forward
+ *           (128-132) and the embedding lookup of PackedGPT.forward (150).
+ */
+int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
+                    const float* w, void* h, int h_dtype, int T, int C, float eps, void* stream);
+/*
+ * act[t][i] = silu(gu[t][2i]) * gu[t][2i+1] for i < F (gu: T rows of 2F fp32,
+ * gate and up interleaved by column, as a gate|up layer with alternating
+ * rows produces them; act NB_F32 or NB_BF16).
+ * Replaces: F.silu(gate(x)) * up(x) over a sequence (generate_torch.py:116-117).
+ */
+int nb_silu_pairs_rows(const float* gu, void* act, int act_dtype, int T, int F, void* stream);
+/*
+ * For tokens t < T at positions pos0 + t: RoPE of the query and key heads of
+ * qkv (T rows of 3 * n_head * head_dim fp32, q | k | v), the rotated keys
+ * and the values appended to the caches, and q_out[t] = rotated q *
+ * head_dim^-0.5 (T rows of n_head * head_dim fp32).  pos0 + T <= ctx,
+ * head_dim even and <= 128.
+ * Replaces: apply_rope and the cache writes of CausalAttention.forward
+ *           (inference/generate_torch.py:48-60, 80-88) for T tokens.
+ */
+int nb_rope_kv_rows(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                    const float* sin_t, int pos0, int T, float* q_out, int n_head, int head_dim,
+                    int ctx, void* stream);
+/*
+ * out[t] = softmax(q[t] . k[0 .. pos0 + t]) . v[0 .. pos0 + t] for every
+ * head (causal: query t sees cache positions up to its own, pos0 + t); q
+ * as nb_rope_kv_rows writes it, out T rows of n_head * head_dim (NB_F32 or
+ * NB_BF16).
+ * Replaces: the masked attention of CausalAttention.forward with the cache
+ *           (inference/generate_torch.py:89-98) for T > 1 queries.
+ */
+int nb_attention_rows(const float* q, const float* k_cache, const float* v_cache, int pos0, int T,
+                      void* out, int out_dtype, int n_head, int head_dim, int ctx, void* stream);
+
+/* ------------------------------------------------------------------------
  * Persistent decode: many greedy tokens of the whole packed decoder in one
  * cooperative launch (one workgroup per CU), the phases of a token separated
  * by grid barriers instead of kernel boundaries, and the packed weights of

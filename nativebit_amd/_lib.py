@@ -71,6 +71,10 @@ SIGNATURES = {
     "nb_attention_step_static": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "nb_attention_static_scratch_bytes": (_L, []),
     "nb_silu_mul": (_I, [_P, _P, _I, _I, _P]),
+    "nb_rmsnorm_rows": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, ctypes.c_float, _P]),
+    "nb_silu_pairs_rows": (_I, [_P, _P, _I, _I, _I, _P]),
+    "nb_rope_kv_rows": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
+    "nb_attention_rows": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P]),
     "nb_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
     "nb_decode_workspace_bytes": (_L, [_P]),
     "nb_decode_persistent": (_I, [_P, _P, _L, _P, _P, _P, _I, _P, _I, _I, _I, _P]),

@@ -557,6 +557,97 @@ int nb_attention_step_static(const float* qkv, float* k_cache, float* v_cache, c
 
 int64_t nb_attention_static_scratch_bytes(void) { return static_attention_scratch_bytes(); }
 
+int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
+                    const float* w, void* h, int h_dtype, int T, int C, float eps, void* stream) {
+    const char* fn = "nb_rmsnorm_rows";
+    if (T < 0 || C < 1) return fail(NB_EINVAL, "%s: T=%d C=%d", fn, T, C);
+    if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(NB_EINVAL, "%s: eps=%g", fn, (double)eps);
+    if (h_dtype != NB_F32 && h_dtype != NB_BF16) return fail(NB_EINVAL, "%s: h_dtype=%d", fn, h_dtype);
+    if (!x || !w || !h) return fail(NB_EINVAL, "%s: NULL x, w or h", fn);
+    if ((emb == nullptr) != (tokens == nullptr)) {
+        return fail(NB_EINVAL, "%s: emb and tokens go together", fn);
+    }
+    if (emb && add) return fail(NB_EINVAL, "%s: an embedding lookup takes no add", fn);
+    if (!aligned(x, 4) || !aligned(w, 4) || (add && !aligned(add, 4)) || (emb && !aligned(emb, 4)) ||
+        (tokens && !aligned(tokens, 4)) || !aligned(h, dtype_size(h_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    if (T == 0) return NB_OK;
+    int st = ensure_device();
+    if (st) return st;
+    return launch_rmsnorm_rows(x, add, emb, tokens, w, h, h_dtype, T, C, eps,
+                               static_cast<hipStream_t>(stream));
+}
+
+int nb_silu_pairs_rows(const float* gu, void* act, int act_dtype, int T, int F, void* stream) {
+    const char* fn = "nb_silu_pairs_rows";
+    if (T < 0 || F < 1) return fail(NB_EINVAL, "%s: T=%d F=%d", fn, T, F);
+    if (act_dtype != NB_F32 && act_dtype != NB_BF16) return fail(NB_EINVAL, "%s: act_dtype=%d", fn, act_dtype);
+    if (!gu || !act) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(gu, 4) || !aligned(act, dtype_size(act_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    if (T == 0) return NB_OK;
+    int st = ensure_device();
+    if (st) return st;
+    return launch_silu_pairs_rows(gu, act, act_dtype, T, F, static_cast<hipStream_t>(stream));
+}
+
+namespace {
+int check_rows_attention(const char* fn, int pos0, int T, int n_head, int head_dim, int ctx) {
+    if (T < 0 || n_head < 1 || ctx < 1 || pos0 < 0) {
+        return fail(NB_EINVAL, "%s: T=%d n_head=%d ctx=%d pos0=%d", fn, T, n_head, ctx, pos0);
+    }
+    if ((int64_t)pos0 + T > ctx) {
+        return fail(NB_EINVAL, "%s: positions %d..%d beyond the cache (ctx=%d)", fn, pos0,
+                    pos0 + T - 1, ctx);
+    }
+    if (head_dim < 2 || head_dim % 2 || head_dim > attention_rows_max_head_dim()) {
+        return fail(NB_EUNSUPPORTED, "%s: head_dim=%d (even, <= %d)", fn, head_dim,
+                    attention_rows_max_head_dim());
+    }
+    return NB_OK;
+}
+}  // namespace
+
+int nb_rope_kv_rows(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                    const float* sin_t, int pos0, int T, float* q_out, int n_head, int head_dim,
+                    int ctx, void* stream) {
+    const char* fn = "nb_rope_kv_rows";
+    int st = check_rows_attention(fn, pos0, T, n_head, head_dim, ctx);
+    if (st) return st;
+    if (!qkv || !k_cache || !v_cache || !cos_t || !sin_t || !q_out) {
+        return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    }
+    if (!aligned(qkv, 4) || !aligned(k_cache, 4) || !aligned(v_cache, 4) || !aligned(cos_t, 4) ||
+        !aligned(sin_t, 4) || !aligned(q_out, 4)) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    if (T == 0) return NB_OK;
+    st = ensure_device();
+    if (st) return st;
+    return launch_rope_kv_rows(qkv, k_cache, v_cache, cos_t, sin_t, pos0, T, q_out, n_head,
+                               head_dim, ctx, static_cast<hipStream_t>(stream));
+}
+
+int nb_attention_rows(const float* q, const float* k_cache, const float* v_cache, int pos0, int T,
+                      void* out, int out_dtype, int n_head, int head_dim, int ctx, void* stream) {
+    const char* fn = "nb_attention_rows";
+    int st = check_rows_attention(fn, pos0, T, n_head, head_dim, ctx);
+    if (st) return st;
+    if (out_dtype != NB_F32 && out_dtype != NB_BF16) return fail(NB_EINVAL, "%s: out_dtype=%d", fn, out_dtype);
+    if (!q || !k_cache || !v_cache || !out) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(q, 4) || !aligned(k_cache, 4) || !aligned(v_cache, 4) ||
+        !aligned(out, dtype_size(out_dtype))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    if (T == 0) return NB_OK;
+    st = ensure_device();
+    if (st) return st;
+    return launch_attention_rows(q, k_cache, v_cache, pos0, T, out, out_dtype, n_head, head_dim,
+                                 ctx, static_cast<hipStream_t>(stream));
+}
+
 int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream) {
     const char* fn = "nb_silu_mul";
     if (n < 1) return fail(NB_EINVAL, "%s: n=%d < 1", fn, n);

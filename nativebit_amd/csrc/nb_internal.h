@@ -154,6 +154,20 @@ int static_attention_scratch(hipStream_t stream, float** work, unsigned** done);
 int static_attention_max_heads();
 int64_t static_attention_scratch_bytes();
 
+// Batched-pass kernels (nb_rows.hip); arguments validated.
+int launch_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
+                        const float* w, void* h, int h_dtype, int T, int C, float eps,
+                        hipStream_t stream);
+int launch_silu_pairs_rows(const float* gu, void* act, int act_dtype, int T, int F,
+                           hipStream_t stream);
+int launch_rope_kv_rows(const float* qkv, float* k_cache, float* v_cache, const float* cos_t,
+                        const float* sin_t, int pos0, int T, float* q_out, int n_head, int D,
+                        int ctx, hipStream_t stream);
+int launch_attention_rows(const float* q, const float* k_cache, const float* v_cache, int pos0,
+                          int T, void* out, int out_dtype, int n_head, int D, int ctx,
+                          hipStream_t stream);
+int attention_rows_max_head_dim();
+
 // Persistent decode (nb_decode_persistent.hip); arguments validated.
 int64_t decode_persistent_workspace_bytes(int C, int H, int F);
 int decode_persistent_limits(int* max_c, int* max_f, int* max_d, int* max_ctx, int* max_heads,

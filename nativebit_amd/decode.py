@@ -262,6 +262,96 @@ class DecodeEngine(_DecoderBase):
         self._advance(1)
         self._launch()
 
+    @torch.no_grad()
+    def prefill(self, prompt_tokens):
+        """Feed the whole prompt as one batched pass -- the reference's
+        prompt forward over T tokens (generate_torch.py:299-302) -- and choose
+        the first generated token: per layer the q|k|v, o, gate|up and down
+        matmuls are packed MFMA contractions over the T rows (nb_gemm_prefill),
+        RoPE and the cache appends are nb_rope_kv_rows, causal attention is
+        nb_attention_rows, and the norms with their residual adds are
+        nb_rmsnorm_rows; the last row's final norm feeds nb_lm_head_argmax.
+        Afterwards the state is that of the per-token path after the last
+        prompt token, so run() continues the sequence."""
+        prompt = [int(t) for t in prompt_tokens]
+        self.reset(prompt)
+        T, C, F, H, D = len(prompt), self.C, self.F, self.H, self.D
+        lib, ck = _lib.load(), _lib.check
+        s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        z, bf16, BF = self._z, torch.bfloat16, _lib.NB_BF16
+        toks = torch.tensor(prompt, dtype=torch.int32, device=self.dev)
+        x, h = z(T, C), z(T, C, dt=bf16)
+        qkv, q, att, o = z(T, 3 * C), z(T, C), z(T, C, dt=bf16), z(T, C)
+        gu, act, dn = z(T, 2 * F), z(T, F, dt=bf16), z(T, C)
+        ln1 = [n[0] for n in self.norms]
+        ck(lib.nb_rmsnorm_rows(_ptr(x), None, _ptr(self.emb_f32), _ptr(toks), _ptr(ln1[0]),
+                               _ptr(h), BF, T, C, self.eps, s))
+        for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
+            ops.gemm_prefill(h, qkv_p, qkv_c, 3 * C, C, out=qkv)
+            ck(lib.nb_rope_kv_rows(_ptr(qkv), _ptr(self.kc[l]), _ptr(self.vc[l]), _ptr(self.cos),
+                                   _ptr(self.sin), 0, T, _ptr(q), H, D, self.ctx, s))
+            ck(lib.nb_attention_rows(_ptr(q), _ptr(self.kc[l]), _ptr(self.vc[l]), 0, T, _ptr(att),
+                                     BF, H, D, self.ctx, s))
+            ops.gemm_prefill(att, o_p, o_c, C, C, out=o)
+            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(o), None, None, _ptr(self.norms[l][1]), _ptr(h),
+                                   BF, T, C, self.eps, s))
+            ops.gemm_prefill(h, gu_p, gu_c, 2 * F, C, out=gu)  # gate, up columns interleaved
+            ck(lib.nb_silu_pairs_rows(_ptr(gu), _ptr(act), BF, T, F, s))
+            ops.gemm_prefill(act, d_p, d_c, C, F, out=dn)
+            w_next = ln1[l + 1] if l + 1 < len(self.fused) else self.ln_f
+            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(dn), None, None, _ptr(w_next), _ptr(h), BF, T,
+                                   C, self.eps, s))
+        # the last prompt token's head: its step writes tokens_out[T - 1] and
+        # leaves position T, as the per-token path would
+        st = _lib.DecodeState(0, T - 1, prompt[-1], T - 1, 0)
+        self.state_t[: ctypes.sizeof(st)].copy_(torch.frombuffer(bytearray(bytes(st)),
+                                                                  dtype=torch.uint8))
+        h_last = h[T - 1]
+        ck(lib.nb_lm_head_argmax(_ptr(h_last), _ptr(self.emb_bf16), _ptr(self.logits),
+                                 _ptr(self.state_t), _ptr(self.tokens), self.max_steps,
+                                 _ptr(self.force), self.n_force, self.V, C, s))
+        self.x.copy_(x[T - 1])
+        self.fed = T
+
+    @torch.no_grad()
+    def generate(self, prompt_tokens, n_generate: int, batched_prompt: bool = True) -> list:
+        """Greedy continuation (generate_torch.py:298-313): the prompt as one
+        batched pass (or, with batched_prompt=False, fed token by token
+        through the decode step), then one graph replay per token."""
+        if not batched_prompt:
+            return super().generate(prompt_tokens, n_generate)
+        n_prompt = len(prompt_tokens)
+        if n_prompt + n_generate > min(self.ctx, self.max_steps):
+            raise ValueError("prompt + generated tokens exceed the context")
+        self.prefill(prompt_tokens)
+        self.run(n_generate - 1)
+        torch.cuda.synchronize()
+        return self.tokens[n_prompt - 1: n_prompt - 1 + n_generate].cpu().tolist()
+
+    @torch.no_grad()
+    def benchmark(self, prompt_tokens, n_generate: int, n_runs: int = 3) -> dict:
+        """Decode tokens/s after the prompt (timed like generate_torch.py:
+        280-320: the prompt pass first, then the continuation is timed), and
+        the prompt pass's own time."""
+        times, prompt_times = [], []
+        for _ in range(n_runs):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            self.prefill(prompt_tokens)   # the prompt, batched; first token chosen
+            torch.cuda.synchronize()
+            prompt_times.append(time.perf_counter() - t0)
+            if self.graph is None:
+                self.capture()
+            t0 = time.perf_counter()
+            self.run(n_generate - 1)      # the rest of the continuation
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        t = sorted(times)[len(times) // 2]
+        tp = sorted(prompt_times)[len(prompt_times) // 2]
+        return {"generate_tps": (n_generate - 1) / t, "per_token_ms": t / (n_generate - 1) * 1e3,
+                "prompt_ms": tp * 1e3, "prompt_tps": len(prompt_tokens) / tp,
+                "runs": len(times)}
+
     def capture(self):
         """Capture one step in a HIP graph (replayed by run())."""
         g = torch.cuda.CUDAGraph()

@@ -1,26 +1,29 @@
-"""Packed NativeBit decoder: the reference's PackedGPT and its loader.
+"""Packed NativeBit decoder: the reference's PackedGPT API on the gfx950
+kernels, and its loader.
 
-Mirrors inference/generate_torch.py:29-277 module for module: RMSNorm
-(29-38), interleaved-pair RoPE (41-60), causal attention with a static KV
-cache (63-106), SwiGLU (109-117), pre-norm blocks (120-132), a tied,
-soft-capped LM head (135-162), ``load_packed_model`` (176-266) and
-``init_kv_cache`` (269-277).  Every quantized linear is a PackedLinear on
-the gfx950 kernels; the non-quantized arithmetic here is plain torch, in
-fp32 as in the reference.  ``nativebit_amd.decode`` runs the same model as
-fused HIP kernels for speed; this module is its functional statement.
+The module names, constructor arguments and forward signatures are those of
+inference/generate_torch.py:29-277 (RMSNorm, precompute_rope / apply_rope,
+CausalAttention with a static cache, SwiGLU, TransformerBlock, PackedGPT,
+load_packed_model, init_kv_cache), so code written against the reference's
+model runs unchanged.  The arithmetic runs in this library's kernels: the
+packed linears are PackedLinear (fused dequant-GEMV for up to 16 rows, a
+device gather + dense GEMM beyond), the norms nb_rmsnorm_rows (with the
+residual add fused into the second norm of a block), RoPE and the cache
+appends nb_rope_kv_rows, attention nb_attention_rows, the SwiGLU product
+nb_silu_pairs_rows.  Activations stay fp32 (the reference's module
+numerics); ``nativebit_amd.decode.DecodeEngine`` runs the same model with
+bf16 GEMV inputs, one HIP graph per token, for speed.
 """
 from __future__ import annotations
 
-import math
-import time
+import ctypes
 from dataclasses import dataclass
 
 import numpy as np
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
-from . import formats, synth
+from . import _lib, formats, synth
 from .linear import PackedLinear
 
 
@@ -39,8 +42,23 @@ class ModelConfig:
     norm_eps: float = 1e-6
 
 
+def _stream(dev) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _rows(x: torch.Tensor, width: int) -> torch.Tensor:
+    """x as contiguous fp32 rows of `width` (a copy when it is not already)."""
+    return x.reshape(-1, width).to(torch.float32).contiguous()
+
+
 class RMSNorm(nn.Module):
-    """x / sqrt(mean(x^2) + eps) * w, in fp32 (generate_torch.py:29-38)."""
+    """Root-mean-square norm of the last dimension times a weight, in fp32
+    (generate_torch.py:29-38), by the row kernel nb_rmsnorm_rows; the result
+    takes x's dtype."""
 
     def __init__(self, dim, eps=1e-6):
         super().__init__()
@@ -48,42 +66,55 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x):
-        dtype = x.dtype
-        norm = torch.sqrt(x.float().pow(2).mean(-1, keepdim=True) + self.eps)
-        return (x.float() / norm * self.weight.float()).to(dtype)
+        C = x.shape[-1]
+        rows = _rows(x, C)
+        out = torch.empty_like(rows)
+        w = self.weight.detach().to(torch.float32).contiguous()
+        _lib.check(_lib.load().nb_rmsnorm_rows(
+            _p(rows), None, None, None, _p(w), _p(out), _lib.NB_F32, rows.shape[0], C,
+            float(self.eps), _stream(x.device)))
+        return out.reshape(x.shape).to(x.dtype)
 
 
 def precompute_rope(dim, max_len, theta=10000.0):
-    """cos/sin tables (max_len, dim/2) in fp32 (generate_torch.py:41-45)."""
-    freqs = 1.0 / (theta ** (torch.arange(0, dim, 2, dtype=torch.float32) / dim))
-    t = torch.arange(max_len, dtype=torch.float32)
-    freqs = torch.outer(t, freqs)
-    return torch.cos(freqs), torch.sin(freqs)
+    """cos / sin tables (max_len, dim / 2) fp32 of the angles pos * theta^(-2i
+    / dim) -- the reference's fp32 arithmetic (generate_torch.py:41-45), so
+    the rotations match it bit for bit."""
+    inv = torch.arange(0, dim, 2, dtype=torch.float32).div(dim)
+    inv = torch.pow(torch.tensor(theta, dtype=torch.float32), inv).reciprocal()
+    ang = torch.arange(max_len, dtype=torch.float32).unsqueeze(1) * inv.unsqueeze(0)
+    return ang.cos(), ang.sin()
 
 
 def apply_rope(q, k, cos, sin, pos_offset=0):
-    """Rotation of (even, odd) pairs (generate_torch.py:48-60)."""
-    dtype = q.dtype
+    """Rotates each (even, odd) pair of the last dimension of q and k (B, H,
+    T, D) by the angles of positions pos_offset .. pos_offset + T - 1
+    (generate_torch.py:48-60), in fp32, results in the inputs' dtype."""
     T = q.shape[2]
-    cos = cos[pos_offset:pos_offset + T][None, None, :, :]
-    sin = sin[pos_offset:pos_offset + T][None, None, :, :]
-    cos2 = cos.repeat_interleave(2, dim=-1)
-    sin2 = sin.repeat_interleave(2, dim=-1)
+    c = cos[pos_offset:pos_offset + T].to(q.device)
+    s_ = sin[pos_offset:pos_offset + T].to(q.device)
 
-    def rotate(x):
-        x1, x2 = x[..., ::2], x[..., 1::2]
-        return torch.stack((-x2, x1), dim=-1).reshape(x.shape)
+    def turn(x):
+        pairs = x.float().unflatten(-1, (-1, 2))
+        a, b = pairs[..., 0], pairs[..., 1]
+        return torch.stack((a * c - b * s_, b * c + a * s_), dim=-1).flatten(-2).to(x.dtype)
 
-    q_rot = (q.float() * cos2 + rotate(q.float()) * sin2).to(dtype)
-    k_rot = (k.float() * cos2 + rotate(k.float()) * sin2).to(dtype)
-    return q_rot, k_rot
+    return turn(q), turn(k)
 
 
 class CausalAttention(nn.Module):
+    """Causal self-attention over a static cache (generate_torch.py:63-106):
+    the packed q|k|v and output projections around nb_rope_kv_rows (RoPE,
+    cache append) and nb_attention_rows (masked softmax over the cache).
+    A cache is (keys [B][H][D][ctx], values [B][H][ctx][D], length), the
+    layout of the GPU decode step; without one the sequence attends to
+    itself from position pos_offset on."""
+
     def __init__(self, n_embd, n_head, context_len, qkv, out_proj, theta=10000.0):
         super().__init__()
         self.n_head = n_head
         self.head_dim = n_embd // n_head
+        self.context_len = context_len
         self.qkv = qkv
         self.out_proj = out_proj
         cos, sin = precompute_rope(self.head_dim, context_len, theta)
@@ -92,46 +123,53 @@ class CausalAttention(nn.Module):
 
     def forward(self, x, kv_cache=None, pos_offset=0):
         B, T, C = x.shape
-        qkv = self.qkv(x)
-        q, k, v = qkv.chunk(3, dim=-1)
-        q = q.reshape(B, T, self.n_head, self.head_dim).transpose(1, 2)
-        k = k.reshape(B, T, self.n_head, self.head_dim).transpose(1, 2)
-        v = v.reshape(B, T, self.n_head, self.head_dim).transpose(1, 2)
+        H, D = self.n_head, self.head_dim
+        dev = x.device
+        qkv = self.qkv(x).reshape(B, T, 3 * C).to(torch.float32).contiguous()
         if kv_cache is not None:
-            pos_offset = kv_cache[2]
-        q, k = apply_rope(q, k, self.cos, self.sin, pos_offset)
-        if kv_cache is not None:
-            k_buf, v_buf, cache_len = kv_cache
-            k_buf[:, :, cache_len:cache_len + T] = k
-            v_buf[:, :, cache_len:cache_len + T] = v
-            new_len = cache_len + T
-            scale = self.head_dim ** -0.5
-            # (b h q d) x (b h d k): batched matmul in fp32 on a contiguous
-            # right operand
-            attn = torch.matmul(q * scale, k_buf.transpose(-1, -2).contiguous())
-            q_pos = cache_len + torch.arange(T, device=x.device)
-            k_pos = torch.arange(k_buf.shape[2], device=x.device)
-            mask = (k_pos[None, :] <= q_pos[:, None]) & (k_pos[None, :] < new_len)
-            attn = attn.masked_fill(~mask[None, None], torch.finfo(attn.dtype).min)
-            out = torch.matmul(F.softmax(attn, dim=-1), v_buf)
-            new_cache = (k_buf, v_buf, new_len)
+            k_buf, v_buf, pos0 = kv_cache
+            ctx = k_buf.shape[-1]
         else:
-            out = F.scaled_dot_product_attention(q, k, v, is_causal=True)
-            new_cache = None
-        out = out.transpose(1, 2).reshape(B, T, C)
-        return self.out_proj(out), new_cache
+            pos0, ctx = pos_offset, pos_offset + T
+            k_buf = torch.zeros(B, H, D, ctx, device=dev)
+            v_buf = torch.zeros(B, H, ctx, D, device=dev)
+        cos, sin = self.cos.to(dev).contiguous(), self.sin.to(dev).contiguous()
+        if pos0 + T > cos.shape[0]:
+            raise ValueError(f"positions up to {pos0 + T} exceed the RoPE tables")
+        q = torch.empty(T, C, device=dev)
+        att = torch.empty(B, T, C, device=dev)
+        lib, s = _lib.load(), _stream(dev)
+        for b in range(B):
+            _lib.check(lib.nb_rope_kv_rows(_p(qkv[b]), _p(k_buf[b]), _p(v_buf[b]), _p(cos),
+                                           _p(sin), pos0, T, _p(q), H, D, ctx, s))
+            _lib.check(lib.nb_attention_rows(_p(q), _p(k_buf[b]), _p(v_buf[b]), pos0, T,
+                                             _p(att[b]), _lib.NB_F32, H, D, ctx, s))
+        out = self.out_proj(att)
+        return out, ((k_buf, v_buf, pos0 + T) if kv_cache is not None else None)
 
 
 class SwiGLU(nn.Module):
+    """down(silu(gate(x)) * up(x)) (generate_torch.py:109-117); the product is
+    nb_silu_pairs_rows over the gate and up outputs side by side."""
+
     def __init__(self, gate, up, down):
         super().__init__()
         self.gate, self.up, self.down = gate, up, down
 
     def forward(self, x):
-        return self.down(F.silu(self.gate(x)) * self.up(x))
+        g, u = self.gate(x), self.up(x)
+        F = g.shape[-1]
+        pairs = torch.stack((g.float(), u.float()), dim=-1).reshape(-1, 2 * F).contiguous()
+        act = torch.empty(pairs.shape[0], F, device=x.device)
+        _lib.check(_lib.load().nb_silu_pairs_rows(_p(pairs), _p(act), _lib.NB_F32,
+                                                  pairs.shape[0], F, _stream(x.device)))
+        return self.down(act.reshape(*g.shape[:-1], F).to(x.dtype))
 
 
 class TransformerBlock(nn.Module):
+    """Pre-norm block (generate_torch.py:120-132): the attention's residual
+    add and the second norm are one nb_rmsnorm_rows (add form)."""
+
     def __init__(self, cfg: ModelConfig, lin: dict):
         super().__init__()
         self.ln1 = RMSNorm(cfg.n_embd, cfg.norm_eps)
@@ -141,10 +179,16 @@ class TransformerBlock(nn.Module):
         self.ffn = SwiGLU(lin["gate"], lin["up"], lin["down"])
 
     def forward(self, x, kv_cache=None, pos_offset=0):
-        attn_out, new_cache = self.attn(self.ln1(x), kv_cache, pos_offset=pos_offset)
-        x = x + attn_out
-        x = x + self.ffn(self.ln2(x))
-        return x, new_cache
+        C = x.shape[-1]
+        a, new_cache = self.attn(self.ln1(x), kv_cache, pos_offset=pos_offset)
+        res = x.reshape(-1, C).to(torch.float32, copy=True)   # becomes x + a (a fresh copy)
+        h = torch.empty_like(res)
+        w2 = self.ln2.weight.detach().to(torch.float32).contiguous()
+        _lib.check(_lib.load().nb_rmsnorm_rows(
+            _p(res), _p(_rows(a, C)), None, None, _p(w2), _p(h), _lib.NB_F32, res.shape[0], C,
+            float(self.ln2.eps), _stream(x.device)))
+        f = self.ffn(h.reshape(x.shape).to(x.dtype))
+        return (res.reshape(x.shape) + f.float()).to(x.dtype), new_cache
 
 
 # order of a block's quantized linears (module order of generate_torch.py:
@@ -153,7 +197,11 @@ LINEAR_NAMES = ("qkv", "out_proj", "gate", "up", "down")
 
 
 class PackedGPT(nn.Module):
-    """generate_torch.py:135-162 with PackedLinear layers."""
+    """The packed decoder (generate_torch.py:135-162): token embedding, the
+    blocks, a final norm and the tied, soft-capped head 30 tanh(l / 30).
+    Activations are fp32 through the packed linears (exact fp32 weights, the
+    reference's module numerics); ``nativebit_amd.decode.DecodeEngine`` runs
+    the same model on bf16 GEMV inputs for speed."""
 
     def __init__(self, cfg: ModelConfig, linears: list, embedding: torch.Tensor):
         super().__init__()
@@ -169,45 +217,46 @@ class PackedGPT(nn.Module):
 
     @torch.no_grad()
     def forward(self, idx, kv_caches=None, pos_offset=0):
-        x = self.embedding(idx)
-        new_caches = []
+        """Logits (B, T, vocab) fp32 of tokens idx (B, T); with kv_caches
+        (from init_kv_cache) the caches are read and extended and the new
+        caches are returned too."""
+        emb = self.embedding.weight
+        x = emb.index_select(0, idx.reshape(-1)).reshape(*idx.shape, emb.shape[1]).float()
+        caches = []
         for i, block in enumerate(self.blocks):
-            cache = kv_caches[i] if kv_caches is not None else None
-            x, new_cache = block(x, cache, pos_offset=pos_offset)
-            new_caches.append(new_cache)
-        x = self.ln_f(x)
-        logits = x.to(self.embedding.weight.dtype) @ self.embedding.weight.T
-        logits = 30.0 * torch.tanh(logits.float() / 30.0)
-        if kv_caches is not None:
-            return logits, new_caches
-        return logits
+            x, c = block(x, kv_caches[i] if kv_caches is not None else None, pos_offset)
+            caches.append(c)
+        h = self.ln_f(x)
+        logits = torch.tanh(h.to(emb.dtype) @ emb.t() / 30.0).float() * 30.0
+        return (logits, caches) if kv_caches is not None else logits
 
 
 def init_kv_cache(model: PackedGPT, batch_size=1, device="cuda", dtype=torch.float32):
-    """Static per-layer K/V buffers (generate_torch.py:269-277)."""
-    head_dim = model.n_embd // model.n_head
-    caches = []
-    for _ in range(model.n_layers):
-        k = torch.zeros(batch_size, model.n_head, model.context_len, head_dim, device=device,
-                        dtype=dtype)
-        caches.append((k, torch.zeros_like(k), 0))
-    return caches
+    """Empty static caches, one (keys [B][H][D][ctx], values [B][H][ctx][D],
+    length 0) per block -- the generate_torch.py:269-277 caches in the GPU
+    decode step's layout (keys transposed); fp32 only."""
+    if dtype != torch.float32:
+        raise ValueError("the caches are fp32")
+    D = model.n_embd // model.n_head
+    shape_k = (batch_size, model.n_head, D, model.context_len)
+    shape_v = (batch_size, model.n_head, model.context_len, D)
+    return [(torch.zeros(shape_k, device=device), torch.zeros(shape_v, device=device), 0)
+            for _ in range(model.n_layers)]
 
 
 @torch.no_grad()
 def greedy_generate(model: PackedGPT, prompt_tokens, n_generate: int, device="cuda"):
-    """Prefill the prompt, then decode greedily with the KV cache; returns
-    the generated token ids (generate_torch.py:298-313)."""
+    """The reference's greedy loop (generate_torch.py:298-313) on the module
+    forward: the prompt as one pass over the caches, then one token per
+    pass, each the argmax of the last logits."""
     caches = init_kv_cache(model, device=device)
-    x = torch.tensor([list(prompt_tokens)], dtype=torch.long, device=device)
-    logits, caches = model(x, kv_caches=caches)
-    token = int(logits[0, -1].argmax())
+    logits, caches = model(torch.tensor([list(prompt_tokens)], device=device), kv_caches=caches)
     out = []
     for _ in range(n_generate):
-        out.append(token)
-        x1 = torch.tensor([[token]], dtype=torch.long, device=device)
-        logits, caches = model(x1, kv_caches=caches)
-        token = int(logits[0, -1].argmax())
+        out.append(int(logits[0, -1].argmax()))
+        if len(out) == n_generate:
+            break
+        logits, caches = model(torch.tensor([[out[-1]]], device=device), kv_caches=caches)
     return out
 
 
@@ -302,24 +351,11 @@ def to_nbpack_params(model: PackedGPT) -> dict:
     return out
 
 
-@torch.no_grad()
 def benchmark(model: PackedGPT, prompt_tokens, n_generate=128, n_runs=3, device="cuda"):
-    """Decode tokens/s with the KV cache (generate_torch.py:280-320)."""
-    greedy_generate(model, prompt_tokens, 2, device)
-    torch.cuda.synchronize()
-    times = []
-    for _ in range(n_runs):
-        caches = init_kv_cache(model, device=device)
-        x = torch.tensor([list(prompt_tokens)], dtype=torch.long, device=device)
-        logits, caches = model(x, kv_caches=caches)
-        torch.cuda.synchronize()
-        token = int(logits[0, -1].argmax())
-        t0 = time.time()
-        for _ in range(n_generate):
-            x1 = torch.tensor([[token]], dtype=torch.long, device=device)
-            logits, caches = model(x1, kv_caches=caches)
-            token = int(logits[0, -1].argmax())
-        torch.cuda.synchronize()
-        times.append(time.time() - t0)
-    t = sum(times) / len(times)
-    return {"generate_tps": round(n_generate / t, 1), "per_token_ms": round(t / n_generate * 1e3, 3)}
+    """Decode tokens/s (the measurement of generate_torch.py:280-320) on the
+    device-resident decoder: the prompt as one batched pass, then one HIP
+    graph replay per generated token."""
+    from .decode import DecodeEngine
+    eng = DecodeEngine(model, max_steps=len(prompt_tokens) + n_generate)
+    r = eng.benchmark(prompt_tokens, n_generate, n_runs)
+    return {"generate_tps": round(r["generate_tps"], 1), "per_token_ms": round(r["per_token_ms"], 3)}

@@ -17,7 +17,12 @@ seed 2024).
   that block and the key and value it cached;
 * the whole 128 + 256 greedy decode: the HIP-graph replays choose the same
   tokens as the same steps launched eagerly, and the same 256 tokens in a
-  second run.
+  second run;
+* the batched prompt pass (DecodeEngine.prefill: packed MFMA GEMMs, row
+  kernels) over 40 tokens on two layers and 16 on all 26 against the
+  oracle under the same bound as the per-token path, and over the 128-token
+  prompt against the per-token path itself: last logits, every cached key
+  and value, the state, the greedy tokens that follow it.
 """
 import copy
 import dataclasses
@@ -81,7 +86,7 @@ def teacher_forced_logits(model, seq):
 BF16 = dict(weight_dtype=torch.bfloat16, act_dtype=torch.bfloat16, head_dtype=torch.bfloat16)
 
 
-def check_vs_oracle(model, seq, label):
+def check_vs_oracle(model, seq, label, prefill=False):
     """Teacher-forced logits of every step against the oracle.
 
     Any change of fp32 summation order moves a few activations across a
@@ -93,6 +98,10 @@ def check_vs_oracle(model, seq, label):
     all-fp32 oracle and pick the oracle's argmax wherever its top two
     logits are 0.05 apart."""
     ours = teacher_forced_logits(model, seq)
+    if prefill:
+        eng = DecodeEngine(model, max_steps=64)
+        eng.prefill(seq)
+        batched = eng.logits.cpu().clone()
     note(f"{label}: GPU steps done; oracle forwards over {len(seq)} tokens")
     ref = R.DecoderRef.from_model(model)
     tokens = torch.tensor([seq])
@@ -108,14 +117,23 @@ def check_vs_oracle(model, seq, label):
         top2 = torch.topk(a[0, t], 2).values
         if float(top2[0] - top2[1]) > 0.05:
             assert int(ours[t].argmax()) == int(a[0, t].argmax()), t
+    if prefill:
+        t = len(seq) - 1
+        e, floor = rel(batched, a[0, t]), rel(b[0, t], a[0, t])
+        note(f"{label}, batched prompt: rel vs oracle {e:.2e} (floor {floor:.2e})")
+        assert e <= 2 * floor + 5e-3, (e, floor)
+        assert rel(batched, f32[0, t]) <= 3e-2
+        top2 = torch.topk(a[0, t], 2).values
+        if float(top2[0] - top2[1]) > 0.05:
+            assert int(batched.argmax()) == int(a[0, t].argmax())
 
 
 def test_decode_2p2b_two_layers_vs_oracle(dev, full_model):
-    check_vs_oracle(truncated(full_model, 2), prompt_4b()[:16], "2 layers")
+    check_vs_oracle(truncated(full_model, 2), prompt_4b()[:40], "2 layers", prefill=True)
 
 
 def test_decode_2p2b_teacher_forced_vs_oracle(dev, full_model):
-    check_vs_oracle(full_model, prompt_4b()[:16], "26 layers")
+    check_vs_oracle(full_model, prompt_4b()[:16], "26 layers", prefill=True)
 
 
 def test_decode_2p2b_layer_by_layer(dev, full_model):
@@ -156,8 +174,8 @@ def test_decode_2p2b_greedy_graph_equals_eager(dev, full_model):
     n_gen = 256
     eng = DecodeEngine(full_model, max_steps=512)
     note("graph replays: 128 prompt + 256 generated")
-    graph_toks = eng.generate(prompt, n_gen)
-    again = eng.generate(prompt, n_gen)
+    graph_toks = eng.generate(prompt, n_gen, batched_prompt=False)
+    again = eng.generate(prompt, n_gen, batched_prompt=False)
     assert again == graph_toks
     note("eager launches of the same steps")
     eng.reset(prompt)
@@ -166,3 +184,38 @@ def test_decode_2p2b_greedy_graph_equals_eager(dev, full_model):
     torch.cuda.synchronize()
     eager = eng.tokens[len(prompt) - 1: len(prompt) - 1 + n_gen].cpu().tolist()
     assert eager == graph_toks
+
+
+def test_prefill_2p2b_vs_per_token(dev, full_model):
+    """The 128-token prompt as one batched pass against the same prompt
+    teacher forced through the per-token step: the two sum in different
+    orders, so they differ by the rounding spread of the oracle test (up to
+    ~2e-2 on the logits after 26 layers); keys and values of every layer
+    and position agree to the same bound, the state exactly."""
+    prompt = prompt_4b()
+    T = len(prompt)
+    a = DecodeEngine(full_model, max_steps=T + 8)
+    a.prefill(prompt)
+    torch.cuda.synchronize()
+    note("batched prompt done; per-token steps")
+    b = DecodeEngine(full_model, max_steps=T + 8)
+    b.reset(prompt)
+    for _ in range(T):
+        b.step()
+    torch.cuda.synchronize()
+    sa, sb = a.state(), b.state()
+    assert (sa["pos"], sa["step"]) == (sb["pos"], sb["step"]) == (T, T)
+    e = rel(a.logits, b.logits)
+    note(f"logits rel {e:.2e}")
+    assert e <= 3e-2
+    top2 = torch.topk(b.logits.float(), 2).values
+    if float(top2[0] - top2[1]) > 0.05:
+        assert sa["token"] == sb["token"]
+    worst = 0.0
+    for l in range(FULL.n_layers):
+        ek = rel(a.kc[l][:, :, :T], b.kc[l][:, :, :T])
+        ev = rel(a.vc[l][:, :T], b.vc[l][:, :T])
+        worst = max(worst, ek, ev)
+        assert ek <= 3e-2 and ev <= 3e-2, (l, ek, ev)
+    note(f"caches: worst rel {worst:.2e}")
+    assert float(a.kc[:, :, :, T:].abs().sum()) == 0
