@@ -11,13 +11,14 @@
 // kernel is shaped for that:
 //
 // * Chunks are whole rows: R = floor(64 / bpr) rows (R * bpr <= 64 blocks,
-//   one block per lane), so any chunk range is row-aligned and every CU gets
-//   a share of even the smallest layer (a 2560 x 2560 o projection is 853
-//   chunks; the batched kernel's row-aligned tiles of 64-block chunks leave
-//   it 160 workgroups, and the 2560 x 6912 down projection 80).
-// * One workgroup per CU, 8 waves; a workgroup's chunks are dealt to its
-//   waves in turn, and each wave requests up to SLOTS of its chunks
-//   (direct-to-LDS, five 1 KiB loads each) at once.
+//   one block per lane), so a lane's column block is the same in every
+//   chunk and its 16 units of staged activations stay in registers for the
+//   whole launch; every CU gets a share of even the smallest layer (a 2560 x
+//   2560 o projection is 853 chunks).
+// * One workgroup per CU, 8 waves; a workgroup owns a contiguous run of
+//   chunks (whole gate|up pairs), dealt to its waves one by one, and each
+//   wave requests up to SLOTS of its chunks (direct-to-LDS, five 1 KiB loads
+//   each) at once.
 // * The activation inputs also arrive by direct-to-LDS loads, issued before
 //   the weight loads: vmcnt counts in issue order, so the wait for them
 //   leaves the weight loads in flight, and no compiler-tracked load sits
@@ -25,8 +26,9 @@
 //   otherwise wait for all of them).  The norm's sum of squares, the bf16
 //   rounding and the staging into the selector layout overlap the weights'
 //   arrival.
-// * Row sums in block order through a per-wave LDS scratch (deterministic,
-//   independent of the grid); y is written after the wave's last chunk.
+// * A chunk's work is its 64 block dot products, one LDS store each; the
+//   row sums (in block order, deterministic, independent of the grid) and
+//   the y epilogue run once per workgroup after its last chunk.
 //
 // Weights are the codebook entries rounded to bf16 (RNE), as the reference's
 // bf16 path (inference/eval_ppl.py:149-174); accumulation is fp32.
@@ -55,8 +57,8 @@ struct RowsArgs {
     const float* norm_w;
     void* y;
     int N, K, bpr, R, nchunks;
-    int unit;           // chunks per scheduling unit (2 keeps gate|up pairs in one wave)
-    int rows_per_wave;  // LDS row sums per wave
+    int unit;           // chunks per scheduling unit (2 keeps gate|up pairs in one workgroup)
+    int wg_chunks;      // LDS dot-product rows (64 floats) per workgroup: its largest share
     int raw_bytes;      // LDS bytes of the raw activation inputs (multiple of 1 KiB)
     int y_mode, y_dtype;
     float eps;
@@ -112,9 +114,8 @@ void gemv_rows_kernel(RowsArgs a) {
     unsigned char* xs = smem;                                   // staged bf16 activations
     unsigned char* raw = xs + bpr * kXColBytes;                 // raw activation inputs
     unsigned char* ring = raw + a.raw_bytes;                    // kWaves x SLOTS slots
-    float* dots = reinterpret_cast<float*>(ring + kWaves * SLOTS * kSlotBytes);  // 64 per wave
-    float* red = dots + kWaves * 64;                            // kWaves floats
-    float* rowbuf = red + kWaves;                               // rows_per_wave per wave
+    float* dots = reinterpret_cast<float*>(ring + kWaves * SLOTS * kSlotBytes);  // 64 per chunk
+    float* red = dots + a.wg_chunks * 64;                       // kWaves floats
 
     // ---- 1. the activation inputs, this wave's share of 1 KiB pieces ------
     const uint32_t raw_lds = lds_addr(raw);
@@ -136,22 +137,14 @@ void gemv_rows_kernel(RowsArgs a) {
         }
     }
 
-    // ---- 2. this wave's chunks and their first loads ------------------------
-    // The workgroup takes a contiguous run of units (a unit is `unit`
-    // consecutive chunks), dealt to its waves in turn: wave w takes units
-    // u0 + w, u0 + w + kWaves, ..., so the waves of a CU (and so its SIMDs)
-    // get equal shares to within one unit.
+    // ---- 2. the workgroup's chunks and this wave's first loads --------------
+    // The workgroup owns chunks [c0, c1) (whole units); wave w takes chunks
+    // c0 + w, c0 + w + kWaves, ...
     const int nunits = (a.nchunks + a.unit - 1) / a.unit;
     const int u0 = (int)((int64_t)blockIdx.x * nunits / gridDim.x);
     const int u1 = (int)((int64_t)(blockIdx.x + 1) * nunits / gridDim.x);
-    const int my_units = u1 - u0 > wave ? (u1 - u0 - wave + kWaves - 1) / kWaves : 0;
-    const int last_unit_chunks = a.nchunks - (nunits - 1) * a.unit;
-    // chunks of this wave: unit k = u0 + wave + k * kWaves holds chunks
-    // k_unit * unit .. (+ unit - 1), fewer in the problem's last unit
-    const int n_full = my_units * a.unit;
-    const bool has_last = my_units > 0 && u0 + wave + (my_units - 1) * kWaves == nunits - 1;
-    const int n = has_last ? n_full - a.unit + last_unit_chunks : n_full;
-    auto chunk_of = [&](int i) { return (u0 + wave + (i / a.unit) * kWaves) * a.unit + i % a.unit; };
+    const int c0 = u0 * a.unit, c1 = min(a.nchunks, u1 * a.unit);
+    const int n = c1 - c0 > wave ? (c1 - c0 - wave + kWaves - 1) / kWaves : 0;
     unsigned char* my_ring = ring + wave * SLOTS * kSlotBytes;
     const uint32_t ring_lds = lds_addr(my_ring);
     const int64_t total_blocks = (int64_t)a.N * bpr;
@@ -169,7 +162,7 @@ void gemv_rows_kernel(RowsArgs a) {
         dma16<0>(dst + kSlotIdx + 1024, min(cp + 1024, clast));
     };
     const int first = min(n, SLOTS);
-    for (int i = 0; i < first; ++i) issue(chunk_of(i), i);
+    for (int i = 0; i < first; ++i) issue(c0 + wave + i * kWaves, i);
 
     // ---- 3. activations: wait for their pieces (the weights stay in flight),
     //         form them in fp32, round to bf16, stage in the selector layout
@@ -216,19 +209,17 @@ void gemv_rows_kernel(RowsArgs a) {
     __syncthreads();
 
     // ---- 4. the wave's chunks: wait, read the slot, refill it, compute ------
-    float* wdots = dots + wave * 64;
-    float* wrows = rowbuf + wave * a.rows_per_wave;
-    const int row_in = lane / bpr;
-    const int col = lane - row_in * bpr;
-    for (int i = 0; i < n; ++i) {
-        const int slot = i % SLOTS;
-        const int c = chunk_of(i);
-        const int rows = min(R, a.N - c * R);
-        const int live = rows * bpr;
-        u32x4_t xv[16];   // the lane's 16 activation units
-        const unsigned char* xb = xs + (lane < live ? col : 0) * kXColBytes;
+    // Lane l takes column block l % bpr of row l / bpr of every chunk (lanes
+    // past R * bpr compute a block nobody reads), so its activation units
+    // are loaded once.
+    u32x4_t xv[16];
+    {
+        const unsigned char* xb = xs + (lane % bpr) * kXColBytes;
 #pragma unroll
         for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
+    }
+    for (int i = 0; i < n; ++i) {
+        const int slot = i % SLOTS;
         const int issued = min(n, i + SLOTS);
         wait_vm_n<(SLOTS - 1) * kLoads>((issued - i - 1) * kLoads);
         const unsigned char* src = my_ring + slot * kSlotBytes;
@@ -236,67 +227,61 @@ void gemv_rows_kernel(RowsArgs a) {
         const u32x4_t* pc = reinterpret_cast<const u32x4_t*>(src + kSlotIdx + 32 * lane);
         const u32x4_t d0 = pi[0], d1 = pi[1], d2 = pi[2], e0 = pc[0], e1 = pc[1];
         wait_lds();
-        if (i + SLOTS < n) issue(chunk_of(i + SLOTS), slot);
+        if (i + SLOTS < n) issue(c0 + wave + (i + SLOTS) * kWaves, slot);
         const f32x4_t acc = block_dot(d0, d1, d2, e0, e1, xv);
-        wdots[lane] = diag_of(acc, lane);
-        wait_lds();
-        // row sums: lane r < rows adds the bpr dot products of row r, 16
-        // independent loads at a time (one LDS latency per 16), in a fixed
-        // order; lanes past the rows read row 0 and store nothing
-        {
-            const float* p = wdots + (lane < rows ? lane : 0) * bpr;
-            float acc[16];
-#pragma unroll
-            for (int q = 0; q < 16; ++q) acc[q] = 0.f;
-            for (int j0 = 0; j0 < bpr; j0 += 16) {
-                float v[16];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) v[q] = p[min(j0 + q, bpr - 1)];
-#pragma unroll
-                for (int q = 0; q < 16; ++q) acc[q] += j0 + q < bpr ? v[q] : 0.f;
-            }
-#pragma unroll
-            for (int h = 8; h > 0; h >>= 1) {
-#pragma unroll
-                for (int q = 0; q < h; ++q) acc[q] += acc[q + h];
-            }
-            if (lane < rows) wrows[i * R + lane] = acc[0];
-        }
-        wait_lds();  // wdots is rewritten by the next chunk
+        dots[(wave + i * kWaves) * 64 + lane] = diag_of(acc, lane);
     }
+    __syncthreads();
 
-    // ---- 5. the wave's rows, written once, unit by unit --------------------
-    for (int k = 0; k * a.unit < n; ++k) {
-        const int c = chunk_of(k * a.unit);
-        const int row0 = c * R;
-        const int nrows = min(a.N, min(c + a.unit, a.nchunks) * R) - row0;
-        const float* ur = wrows + k * a.unit * R;
-        if (a.y_mode == NB_Y_SILU_PAIRS) {
-            // rows 2i, 2i+1 are gate row i and up row i (row0 and nrows are even)
-            bf16_bits* act = static_cast<bf16_bits*>(a.y) + row0 / 2;
-            for (int q = lane; q < nrows / 2; q += 64) {
-                const float g = ur[2 * q], u = ur[2 * q + 1];
-                act[q] = f32_to_bf16_rne((g / (1.0f + __expf(-g))) * u);
-            }
-        } else {
-            for (int r = lane; r < nrows; r += 64) {
-                const float v = ur[r];
-                const int row = row0 + r;
-                if (a.y_dtype == NB_BF16) {
-                    *as_global_mut(static_cast<bf16_bits*>(a.y) + row) = f32_to_bf16_rne(v);
-                } else if (a.y_mode == NB_Y_ADD) {
-                    float* yp = static_cast<float*>(a.y) + row;
-                    *as_global_mut(yp) = *as_global(yp) + v;   // the row is this wave's alone
-                } else {
-                    *as_global_mut(static_cast<float*>(a.y) + row) = v;
-                }
+    // ---- 5. row sums and y, once per workgroup ------------------------------
+    // Row r0 + j is row j % R of local chunk j / R; its bpr dot products are
+    // added in block order into 16 partial sums, then a fixed tree.
+    const int r0 = c0 * R;
+    const int nrows = min(a.N, c1 * R) - r0;
+    auto row_sum = [&](int j) -> float {
+        const float* p = dots + (j / R) * 64 + (j % R) * bpr;
+        float acc[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) acc[q] = 0.f;
+        for (int j0 = 0; j0 < bpr; j0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) v[q] = p[min(j0 + q, bpr - 1)];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[q] += j0 + q < bpr ? v[q] : 0.f;
+        }
+#pragma unroll
+        for (int h = 8; h > 0; h >>= 1) {
+#pragma unroll
+            for (int q = 0; q < h; ++q) acc[q] += acc[q + h];
+        }
+        return acc[0];
+    };
+    if (a.y_mode == NB_Y_SILU_PAIRS) {
+        // rows 2i, 2i+1 are gate row i and up row i (r0 and nrows are even)
+        bf16_bits* act = static_cast<bf16_bits*>(a.y) + r0 / 2;
+        for (int q = tid; q < nrows / 2; q += kThreads) {
+            const float g = row_sum(2 * q), u = row_sum(2 * q + 1);
+            act[q] = f32_to_bf16_rne((g / (1.0f + __expf(-g))) * u);
+        }
+    } else {
+        for (int j = tid; j < nrows; j += kThreads) {
+            const float v = row_sum(j);
+            const int row = r0 + j;
+            if (a.y_dtype == NB_BF16) {
+                *as_global_mut(static_cast<bf16_bits*>(a.y) + row) = f32_to_bf16_rne(v);
+            } else if (a.y_mode == NB_Y_ADD) {
+                float* yp = static_cast<float*>(a.y) + row;
+                *as_global_mut(yp) = *as_global(yp) + v;   // the row is this workgroup's alone
+            } else {
+                *as_global_mut(static_cast<float*>(a.y) + row) = v;
             }
         }
     }
 }
 
 struct RowsShape {
-    int R, nchunks, unit, G, rows_per_wave, raw_bytes, slots;
+    int R, nchunks, unit, G, wg_chunks, raw_bytes, slots;
     size_t lds;
 };
 
@@ -305,18 +290,17 @@ RowsShape rows_shape(const StreamProblem& p) {
     const int bpr = p.K / 128;
     s.R = 64 / bpr;
     s.nchunks = (p.N + s.R - 1) / s.R;
-    // gate|up pairs must not be split between waves: with R odd, two chunks
-    // (an even number of rows) are the unit of the split
+    // gate|up pairs must not be split between workgroups: with R odd, two
+    // chunks (an even number of rows) are the unit of the split
     s.unit = (p.y_mode == NB_Y_SILU_PAIRS && (s.R & 1)) ? 2 : 1;
     const int nunits = (s.nchunks + s.unit - 1) / s.unit;
-    s.G = std::max(1, std::min(device_cu_count(), (nunits + kWaves - 1) / kWaves));
-    const int per_wg = (nunits + s.G - 1) / s.G;   // the largest workgroup share
-    s.rows_per_wave = (per_wg + kWaves - 1) / kWaves * s.unit * s.R;
+    s.G = std::max(1, std::min(device_cu_count(), nunits));
+    s.wg_chunks = (nunits + s.G - 1) / s.G * s.unit;   // the largest workgroup share
     // bf16 x; or fp32 x and a second fp32 input, each from a whole piece
     s.raw_bytes = p.x_mode == NB_X_BF16 ? (2 * p.K + 1023) / 1024 * 1024
                                         : 2 * ((4 * p.K + 1023) / 1024 * 1024);
-    const size_t fixed = (size_t)bpr * kXColBytes + s.raw_bytes + (size_t)kWaves * 64 * 4 +
-                         (size_t)kWaves * 4 + (size_t)kWaves * s.rows_per_wave * 4;
+    const size_t fixed = (size_t)bpr * kXColBytes + s.raw_bytes + (size_t)s.wg_chunks * 64 * 4 +
+                         (size_t)kWaves * 4;
     s.slots = fixed + (size_t)kWaves * 3 * kSlotBytes <= (size_t)device_lds_bytes() ? 3 : 2;
     s.lds = fixed + (size_t)kWaves * s.slots * kSlotBytes;
     return s;
@@ -354,7 +338,7 @@ int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream) {
     a.R = s.R;
     a.nchunks = s.nchunks;
     a.unit = s.unit;
-    a.rows_per_wave = s.rows_per_wave;
+    a.wg_chunks = s.wg_chunks;
     a.raw_bytes = s.raw_bytes;
     a.y_mode = p.y_mode;
     a.y_dtype = y_dtype;
