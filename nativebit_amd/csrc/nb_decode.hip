@@ -417,6 +417,217 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step2_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// attention in 256-position tiles, head_dim 128 (the decode model's shape)
+// ---------------------------------------------------------------------------
+// Workgroup (hd, s) of 512 threads takes positions [256 s, 256 s + 256) of
+// head hd; only ceil((pos + 1) / 256) tiles are in use, so up to 256 cached
+// positions a head is one workgroup and no split combine runs at all.  All
+// global loads are issued before the first is used, as 16-byte loads (32
+// per thread): keys as (4 positions x 16 dimensions) per thread, values as
+// (16 positions x 4 dimensions), so one memory latency and the tile's bytes
+// bound the launch.  Scores: 8 partial sums over 16 dimensions, added in
+// order; softmax partials per wave of 64 positions (max, sum of exp); the
+// weighted values per group of 16 positions, merged in group order with the
+// waves' factors exp(m_w - M).  With more than one tile in use, each writes
+// (M, L, O) and the last to finish (agent-scope counter) merges them as
+// attention_step2_kernel does.  Keys [n_head][128][ctx] and values
+// [n_head][ctx][128] fp32, ctx % 4 == 0, 16-byte aligned.
+constexpr int kTileD = 128;
+constexpr int kTilePos = 256;
+constexpr int kTileThreads = 512;
+static_assert(kTilePos * 4 >= kMaxCtx, "tiles cover the context");
+
+__global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
+    const float* __restrict__ qkv, float* __restrict__ k_cache, float* __restrict__ v_cache,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t,
+    const nb_decode_state* __restrict__ st, float* __restrict__ work, unsigned* __restrict__ done,
+    void* __restrict__ out, int out_dtype, int n_head, int ctx) {
+    typedef __attribute__((ext_vector_type(4))) float f4;
+    constexpr int D = kTileD;
+    __shared__ __align__(16) float qs[D], kn[D], vn[D];
+    __shared__ __align__(16) float sc[8][kTilePos];
+    __shared__ __align__(16) float pl[kTilePos];
+    __shared__ __align__(16) float oh[16][D];
+    __shared__ float wm[4], wl[4];
+    __shared__ unsigned last;
+    const int hd = blockIdx.x, s = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int pos = st->pos;
+    if (pos < 0 || pos >= ctx) return;  // past the cache: nothing to do
+    const int n = pos + 1;
+    const int S = (n + kTilePos - 1) / kTilePos;  // tiles in use
+    if (s >= S) return;
+    const int t0 = s * kTilePos, len = min(kTilePos, n - t0);
+    const int C = n_head * D;
+    const float scale = 1.0f / sqrtf((float)D);
+
+    // ---- loads: the new q, k, v and RoPE row; the tile's keys and values
+    //      (positions past the tile's last one read that one again)
+    float q0 = 0.f, q1 = 0.f, k0 = 0.f, k1 = 0.f, c = 0.f, sn = 0.f, v0 = 0.f;
+    if (tid < D / 2) {
+        q0 = qkv[hd * D + 2 * tid];
+        q1 = qkv[hd * D + 2 * tid + 1];
+        k0 = qkv[C + hd * D + 2 * tid];
+        k1 = qkv[C + hd * D + 2 * tid + 1];
+        c = cos_t[(int64_t)pos * (D / 2) + tid];
+        sn = sin_t[(int64_t)pos * (D / 2) + tid];
+    }
+    if (tid < D) v0 = qkv[2 * C + hd * D + tid];
+    const int pq = tid & 63, dg = wave;                  // keys: 4 positions, 16 dims
+    const int tk = t0 + min(4 * pq, (len - 1) & ~3);
+    const float* kt = k_cache + (int64_t)hd * D * ctx;
+    f4 kr[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+        kr[j] = *reinterpret_cast<const f4*>(kt + (int64_t)(16 * dg + j) * ctx + tk);
+    const int dq = tid & 31, g = tid >> 5;               // values: 16 positions, 4 dims
+    const float* vc = v_cache + (int64_t)hd * ctx * D;
+    f4 vr[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int tt = t0 + min(16 * g + j, len - 1);
+        vr[j] = *reinterpret_cast<const f4*>(vc + (int64_t)tt * D + 4 * dq);
+    }
+
+    // ---- RoPE of the new query and key, then the reference's (q * scale)
+    if (tid < D / 2) {
+        qs[2 * tid] = __fmul_rn(__fadd_rn(__fmul_rn(q0, c), __fmul_rn(-q1, sn)), scale);
+        qs[2 * tid + 1] = __fmul_rn(__fadd_rn(__fmul_rn(q1, c), __fmul_rn(q0, sn)), scale);
+        kn[2 * tid] = __fadd_rn(__fmul_rn(k0, c), __fmul_rn(-k1, sn));
+        kn[2 * tid + 1] = __fadd_rn(__fmul_rn(k1, c), __fmul_rn(k0, sn));
+    }
+    if (tid < D) vn[tid] = v0;
+    __syncthreads();
+    if (s == S - 1 && tid < D) {  // the tile holding pos appends the new key and value
+        k_cache[((int64_t)hd * D + tid) * ctx + pos] = kn[tid];
+        v_cache[((int64_t)hd * ctx + pos) * D + tid] = vn[tid];
+    }
+    // the cache did not hold position pos yet: its key and value come from LDS
+    if (pos >= tk && pos < tk + 4) {
+        const int i = pos - tk;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float v = kn[16 * dg + j];
+            kr[j].x = i == 0 ? v : kr[j].x;
+            kr[j].y = i == 1 ? v : kr[j].y;
+            kr[j].z = i == 2 ? v : kr[j].z;
+            kr[j].w = i == 3 ? v : kr[j].w;
+        }
+    }
+    if (s == S - 1) {  // (positions past the tile's end were read as pos too)
+        const f4 nv = *reinterpret_cast<const f4*>(vn + 4 * dq);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            if (t0 + min(16 * g + j, len - 1) == pos) vr[j] = nv;
+        }
+    }
+
+    // ---- scores: this thread's 4 positions over its 16 dimensions
+    {
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+            const f4 qv = *reinterpret_cast<const f4*>(qs + 16 * dg + 4 * j4);
+            acc += qv.x * kr[4 * j4];
+            acc += qv.y * kr[4 * j4 + 1];
+            acc += qv.z * kr[4 * j4 + 2];
+            acc += qv.w * kr[4 * j4 + 3];
+        }
+        *reinterpret_cast<f4*>(&sc[dg][4 * pq]) = acc;
+    }
+    __syncthreads();
+    if (wave < 4) {  // position tid: its score, the wave's max and sum of exp
+        float sv = -INFINITY;
+        if (tid < len) {
+            sv = 0.f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sv += sc[k][tid];
+        }
+        const float m = wave_max(sv);
+        const float e = tid < len ? __expf(sv - m) : 0.f;
+        pl[tid] = e;
+        const float l = wave_sum(e);
+        if (lane == 0) {
+            wm[wave] = m;
+            wl[wave] = l;
+        }
+    }
+    __syncthreads();
+    // ---- weighted values of this thread's 16 positions, 4 dimensions
+    {
+        f4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j4 = 0; j4 < 4; ++j4) {
+            const f4 pv = *reinterpret_cast<const f4*>(pl + 16 * g + 4 * j4);
+            o += pv.x * vr[4 * j4];
+            o += pv.y * vr[4 * j4 + 1];
+            o += pv.z * vr[4 * j4 + 2];
+            o += pv.w * vr[4 * j4 + 3];
+        }
+        *reinterpret_cast<f4*>(&oh[g][4 * dq]) = o;
+    }
+    __syncthreads();
+    float* wk = work + ((int64_t)hd * kAttnSplits + s) * (kMaxHeadDim + 2);
+    if (tid < D) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w]);
+        float f[4], L = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            f[w] = wm[w] == -INFINITY ? 0.f : __expf(wm[w] - M);
+            L += f[w] * wl[w];
+        }
+        float O = 0.f;
+#pragma unroll
+        for (int gg = 0; gg < 16; ++gg) O += f[gg >> 2] * oh[gg][tid];
+        if (S == 1) {
+            store_act(out, out_dtype, hd * D + tid, O / L);
+        } else {
+            put_agent(wk + 2 + tid, O);
+            if (tid == 0) {
+                put_agent(wk, M);
+                put_agent(wk + 1, L);
+            }
+        }
+    }
+    if (S == 1) return;
+    // ---- more than one tile: the last workgroup of the head merges them
+    wait_stores();
+    __syncthreads();
+    if (tid == 0) {
+        last = __hip_atomic_fetch_add(done + hd, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       (unsigned)(S - 1)
+                   ? 1u
+                   : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
+    if (tid < D) {
+        float mj[4], lj[4], oj[4];
+        float M = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float* pj = base + j * (kMaxHeadDim + 2);
+            mj[j] = j < S ? get_agent(pj) : -INFINITY;
+            lj[j] = j < S ? get_agent(pj + 1) : 0.f;
+            oj[j] = j < S ? get_agent(pj + 2 + tid) : 0.f;
+            M = fmaxf(M, mj[j]);
+        }
+        float L = 0.f, O = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float fj = mj[j] == -INFINITY ? 0.f : __expf(mj[j] - M);
+            L += fj * lj[j];
+            O += fj * oj[j];
+        }
+        store_act(out, out_dtype, hd * D + tid, O / L);
+    }
+    if (tid == 0) done[hd] = 0u;  // ready for the next step
+}
+
+// ---------------------------------------------------------------------------
 // silu(gate) * up
 // ---------------------------------------------------------------------------
 __global__ void silu_mul_kernel(const float* __restrict__ gu, void* __restrict__ act, int dtype,
@@ -591,7 +802,12 @@ int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, cons
                           const float* sin_t, const nb_decode_state* st, float* work,
                           unsigned* done, void* out, int out_dtype, int n_head, int head_dim,
                           int ctx, hipStream_t stream) {
-    if (head_dim <= kAttn2MaxD) {
+    if (head_dim == kTileD && ctx % 4 == 0 && reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(v_cache) % 16 == 0) {
+        hipLaunchKernelGGL(attention_tile_kernel, dim3(n_head, kMaxCtx / kTilePos),
+                           dim3(kTileThreads), 0, stream, qkv, k_cache, v_cache, cos_t, sin_t, st,
+                           work, done, out, out_dtype, n_head, ctx);
+    } else if (head_dim <= kAttn2MaxD) {
         hipLaunchKernelGGL(attention_step2_kernel, dim3(n_head, kAttnSplits), dim3(kAttnThreads),
                            0, stream, qkv, k_cache, v_cache, cos_t, sin_t, st, work, done, out,
                            out_dtype, n_head, head_dim, ctx);

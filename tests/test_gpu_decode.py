@@ -114,7 +114,8 @@ def torch_attention(qkv, kc, vc, pos, H, D, ctx):
     return out, kc, vc
 
 
-@pytest.mark.parametrize("H,D,ctx", [(20, 128, 80), (4, 64, 80), (2, 32, 80), (20, 128, 1024)])
+@pytest.mark.parametrize("H,D,ctx", [(20, 128, 80), (4, 64, 80), (2, 32, 80), (20, 128, 1024),
+                                     (3, 128, 300), (2, 128, 82)])
 def test_attention_step(dev, H, D, ctx):
     lib = _lib.load()
     g = torch.Generator().manual_seed(H * 100 + D)
@@ -125,7 +126,8 @@ def test_attention_step(dev, H, D, ctx):
     done = torch.zeros(H, dtype=torch.int32, device=dev)
     kd, vd = kc.transpose(1, 2).contiguous().to(dev), vc.to(dev)   # keys [H][D][ctx]
     cosd, sind = cos.to(dev), sin.to(dev)
-    for pos in sorted({0, 1, 15, 16, 17, 63, ctx // 2, ctx - 1}):
+    for pos in sorted(p for p in {0, 1, 15, 16, 17, 63, 255, 256, 257, 511, 767, 768, ctx // 2,
+                                  ctx - 1} if p < ctx):
         note(f"attention H={H} D={D} pos={pos}")
         qkv = torch.randn(3 * H * D, generator=g)
         qkvd = qkv.to(dev)
