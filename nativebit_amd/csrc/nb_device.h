@@ -50,6 +50,44 @@ __device__ __forceinline__ T stream_load(const T* p) {
 #endif
 }
 
+// Cross-lane reductions by DPP.  A ds_bpermute-based butterfly (what
+// __shfl_xor compiles to) is six dependent LDS round trips per reduction;
+// these are register moves within each row of 16 lanes plus four lane
+// reads.  Every lane gets the same value; all lanes taking part must be
+// active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_value(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// Sum / max over each row of 16 lanes (pairs, quads, half-rows, rows).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm(1, 0, 3, 2)
+    v += dpp_mov<0x4E>(v);   // quad_perm(2, 3, 0, 1)
+    v += dpp_mov<0x141>(v);  // row_half_mirror
+    v += dpp_mov<0x140>(v);  // row_mirror
+    return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_mov<0xB1>(v));
+    v = fmaxf(v, dpp_mov<0x4E>(v));
+    v = fmaxf(v, dpp_mov<0x141>(v));
+    v = fmaxf(v, dpp_mov<0x140>(v));
+    return v;
+}
+// Sum / max over the 64 lanes of a wave (row totals added in row order).
+__device__ __forceinline__ float wave64_sum(float v) {
+    v = row16_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+__device__ __forceinline__ float wave64_max(float v) {
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)),
+                 fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
 // f rounded to the nearest bfloat16 (ties to even), kept as a float.
 __device__ __forceinline__ float round_bf16(float f) {
     return bf16_to_f32(f32_to_bf16_rne(f));

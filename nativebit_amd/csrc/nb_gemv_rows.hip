@@ -64,11 +64,7 @@ struct RowsArgs {
     float eps;
 };
 
-__device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wsum(float v) { return wave64_sum(v); }
 
 // Halfword position of element e (0..7) of 8-element group g (0..15) of a
 // column block in the staged layout of nb_stream_common.h (stage_unit).
@@ -161,48 +157,80 @@ void gemv_rows_kernel(RowsArgs a) {
         dma16<0>(dst + kSlotIdx, min(cp, clast));
         dma16<0>(dst + kSlotIdx + 1024, min(cp + 1024, clast));
     };
+    // One chunk's loads go out behind the activation pieces, the other slots'
+    // once the pieces are in: the pieces (which every workgroup needs before
+    // it can compute) then do not queue behind the whole weight burst.
     const int first = min(n, SLOTS);
-    for (int i = 0; i < first; ++i) issue(c0 + wave + i * kWaves, i);
+    const int early = min(first, 1);
+    for (int i = 0; i < early; ++i) issue(c0 + wave + i * kWaves, i);
 
     // ---- 3. activations: wait for their pieces (the weights stay in flight),
     //         form them in fp32, round to bf16, stage in the selector layout
-    wait_vm_n<SLOTS * kLoads>(first * kLoads);
+    wait_vm_n<SLOTS * kLoads>(early * kLoads);
+    for (int i = early; i < first; ++i) issue(c0 + wave + i * kWaves, i);
     __syncthreads();  // every wave's pieces are in LDS
     const int ng = K >> 3;
     constexpr int kMaxG = (kMaxK / 8 + kThreads - 1) / kThreads;
-    float norm = 1.f;
-    if constexpr (XMODE == NB_X_RMSNORM) {
-        const float* xf = reinterpret_cast<const float*>(raw);
-        float ss = 0.f;
-        for (int i = tid; i < K; i += kThreads) ss += xf[i] * xf[i];
-        ss = wsum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float t = 0.f;
-        for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
-        norm = sqrtf(t / (float)K + a.eps);
-    }
     uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
+    if constexpr (XMODE == NB_X_BF16) {
 #pragma unroll
-    for (int j = 0; j < kMaxG; ++j) {
-        const int g = tid + j * kThreads;
-        if (g < ng) {
-            uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
+        for (int j = 0; j < kMaxG; ++j) {
+            const int g = tid + j * kThreads;
+            if (g < ng) {
+                uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                uint16_t v;
-                if constexpr (XMODE == NB_X_BF16) {
-                    v = reinterpret_cast<const uint16_t*>(raw)[8 * g + e];
-                } else {
-                    const float xv = reinterpret_cast<const float*>(raw)[8 * g + e];
-                    const float sv = reinterpret_cast<const float*>(raw + a.raw_bytes / 2)[8 * g + e];
+                for (int e = 0; e < 8; ++e)
+                    col[staged_half(g & 15, e)] = reinterpret_cast<const uint16_t*>(raw)[8 * g + e];
+            }
+        }
+    } else {
+        // each thread's groups of 8 inputs, read once into registers
+        typedef __attribute__((ext_vector_type(4))) float f4;
+        const f4* xf4 = reinterpret_cast<const f4*>(raw);
+        const f4* sf4 = reinterpret_cast<const f4*>(raw + a.raw_bytes / 2);
+        f4 xr[kMaxG][2], sr[kMaxG][2];
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxG; ++j) {
+            const int g = tid + j * kThreads;
+            const int gg = g < ng ? g : 0;
+            xr[j][0] = xf4[2 * gg];
+            xr[j][1] = xf4[2 * gg + 1];
+            sr[j][0] = sf4[2 * gg];
+            sr[j][1] = sf4[2 * gg + 1];
+            if (XMODE == NB_X_RMSNORM && g < ng) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    ss += xr[j][h].x * xr[j][h].x + xr[j][h].y * xr[j][h].y +
+                          xr[j][h].z * xr[j][h].z + xr[j][h].w * xr[j][h].w;
+            }
+        }
+        float norm = 1.f;
+        if constexpr (XMODE == NB_X_RMSNORM) {
+            ss = wsum(ss);
+            if (lane == 0) red[wave] = ss;
+            __syncthreads();
+            float t = 0.f;
+            for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
+            norm = sqrtf(t / (float)K + a.eps);
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxG; ++j) {
+            const int g = tid + j * kThreads;
+            if (g < ng) {
+                uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
+                const float xv[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
+                                     xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
+                const float sv[8] = {sr[j][0].x, sr[j][0].y, sr[j][0].z, sr[j][0].w,
+                                     sr[j][1].x, sr[j][1].y, sr[j][1].z, sr[j][1].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
                     // RMSNorm.forward's (x / norm) * w, generate_torch.py:37; silu(g) * u,
                     // 116-117 (exp(-g) by v_exp_f32, a few ulp, below the bf16 rounding)
-                    const float r = XMODE == NB_X_RMSNORM ? (xv / norm) * sv
-                                                          : (xv / (1.0f + __expf(-xv))) * sv;
-                    v = f32_to_bf16_rne(r);
+                    const float r = XMODE == NB_X_RMSNORM ? (xv[e] / norm) * sv[e]
+                                                          : (xv[e] / (1.0f + __expf(-xv[e]))) * sv[e];
+                    col[staged_half(g & 15, e)] = f32_to_bf16_rne(r);
                 }
-                col[staged_half(g & 15, e)] = v;
             }
         }
     }

@@ -124,11 +124,7 @@ struct Meta {
     bool valid;
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave64_sum(v); }
 
 // Halfword position, inside a column block's staged activations, of
 // element e (0..7) of 8-element group g (0..15) of the block: the group's

@@ -31,11 +31,7 @@ __device__ __forceinline__ void store_out(void* p, int dtype, int64_t i, float v
     }
 }
 
-__device__ __forceinline__ float wsum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wsum(float v) { return wave64_sum(v); }
 
 // ---------------------------------------------------------------------------
 // rmsnorm of T rows, one workgroup per row
@@ -176,8 +172,7 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
             tmax = fmaxf(tmax, s[j]);
         }
         // the 16 threads of a query (consecutive lanes) agree on its tile max
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off, 16));
+        tmax = row16_max(tmax);
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = m_new == -INFINITY ? 1.f : __expf(m_run - m_new);
         float lsum = 0.f;
@@ -187,8 +182,7 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
             ps[sq][sp + 16 * j] = e;
             lsum += e;
         }
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) lsum += __shfl_xor(lsum, off, 16);
+        lsum = row16_sum(lsum);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         __syncthreads();
