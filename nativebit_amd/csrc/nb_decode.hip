@@ -634,16 +634,19 @@ __global__ void silu_mul_kernel(const float* __restrict__ gu, void* __restrict__
 // ---------------------------------------------------------------------------
 // tied LM head, soft cap, greedy argmax, position advance
 // ---------------------------------------------------------------------------
-// A wave takes kHeadRows rows at a time: lane i reads 16-byte pieces
-// i, i + 64, ... of each row (bf16), with the rows' loads of one piece in
-// flight together, against h staged in LDS as fp32.  The argmax key is
+// One workgroup per CU (fewer workgroups: fewer same-address atomics at the
+// end); a wave takes kHeadRows rows at a time and has all their 16-byte
+// pieces of a kHeadSpan-column span in flight together (lane i: pieces i,
+// i + 64, ...), against h staged in LDS as fp32.  The argmax key is
 // (order-preserving bits of the capped logit) << 32 | (0xffffffff - row),
 // so the largest key is the first row with the largest value -- torch's
 // argmax -- whatever the order of the atomics.  The last workgroup to
 // finish (atomic counter) turns the key into the next token.
-constexpr int kHeadThreads = 256;
+constexpr int kHeadThreads = 512;
 constexpr int kHeadMaxC = 8192;
-constexpr int kHeadRows = 8;
+constexpr int kHeadRows = 4;
+constexpr int kHeadPieces = 5;                     // per lane and row in one span
+constexpr int kHeadSpan = 64 * 8 * kHeadPieces;    // 2560 columns
 
 __device__ __forceinline__ uint32_t orderable(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -654,7 +657,8 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
     const bf16_bits* __restrict__ h, const bf16_bits* __restrict__ emb, float* __restrict__ logits,
     nb_decode_state* __restrict__ st, int32_t* __restrict__ tokens_out, int tokens_cap,
     const int32_t* __restrict__ force, int n_force, int V, int C) {
-    __shared__ float hs[kHeadMaxC];
+    typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+    __shared__ __align__(16) float hs[kHeadMaxC];
     __shared__ unsigned long long wkey[kHeadThreads / 64];
     __shared__ unsigned last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -662,31 +666,39 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
     __syncthreads();
     unsigned long long best = 0ull;
     const int nwaves = gridDim.x * (kHeadThreads / 64);
-    // kHeadRows rows per wave at a time, their loads issued together
     for (int r0 = (blockIdx.x * (kHeadThreads / 64) + wave) * kHeadRows; r0 < V;
          r0 += nwaves * kHeadRows) {
         float acc[kHeadRows];
 #pragma unroll
         for (int j = 0; j < kHeadRows; ++j) acc[j] = 0.f;
-        for (int c = lane * 8; c < C; c += 512) {
-            typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
-            u32x4_t v[kHeadRows];
+        for (int c0 = 0; c0 < C; c0 += kHeadSpan) {
+            u32x4_t v[kHeadRows][kHeadPieces];
 #pragma unroll
             for (int j = 0; j < kHeadRows; ++j) {
                 const int r = min(r0 + j, V - 1);  // rows past V repeat the last one
-                v[j] = __builtin_nontemporal_load(
-                    reinterpret_cast<const u32x4_t*>(emb + (int64_t)r * C + c));
+#pragma unroll
+                for (int q = 0; q < kHeadPieces; ++q) {
+                    const int c = min(c0 + (q * 64 + lane) * 8, C - 8);  // past C: unused
+                    v[j][q] = __builtin_nontemporal_load(
+                        reinterpret_cast<const u32x4_t*>(emb + (int64_t)r * C + c));
+                }
             }
-            float hv[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) hv[e] = hs[c + e];
+            for (int q = 0; q < kHeadPieces; ++q) {
+                const int c = c0 + (q * 64 + lane) * 8;
+                if (c < C) {
+                    const float4 h0 = *reinterpret_cast<const float4*>(hs + c);
+                    const float4 h1 = *reinterpret_cast<const float4*>(hs + c + 4);
+                    const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
 #pragma unroll
-            for (int j = 0; j < kHeadRows; ++j) {
-                const uint32_t wv[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+                    for (int j = 0; j < kHeadRows; ++j) {
+                        const uint32_t wv[4] = {v[j][q].x, v[j][q].y, v[j][q].z, v[j][q].w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    acc[j] += hv[2 * e] * __uint_as_float(wv[e] << 16);
-                    acc[j] += hv[2 * e + 1] * __uint_as_float(wv[e] & 0xffff0000u);
+                        for (int e = 0; e < 4; ++e) {
+                            acc[j] += hv[2 * e] * __uint_as_float(wv[e] << 16);
+                            acc[j] += hv[2 * e + 1] * __uint_as_float(wv[e] & 0xffff0000u);
+                        }
+                    }
                 }
             }
         }
@@ -821,7 +833,7 @@ int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_deco
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                           int V, int C, hipStream_t stream) {
     const int rows_per_block = kHeadRows * (kHeadThreads / 64);
-    const int blocks = std::min(1024, (V + rows_per_block - 1) / rows_per_block);
+    const int blocks = std::max(1, std::min(device_cu_count(), (V + rows_per_block - 1) / rows_per_block));
     hipLaunchKernelGGL(lm_head_argmax_kernel, dim3(blocks), dim3(kHeadThreads), 0, stream,
                        static_cast<const bf16_bits*>(h), static_cast<const bf16_bits*>(emb), logits,
                        st, tokens_out, tokens_cap, force, n_force, V, C);
