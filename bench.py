@@ -86,6 +86,8 @@ def parse():
                    help="skip the decode / prefill / skinny / sweep configurations")
     p.add_argument("--extra", default="config0,decode,prefill,skinny,sweep,quantize,codec",
                    help="comma list of extra configurations to run")
+    p.add_argument("--decode-tokens", type=int, default=256,
+                   help="tokens generated after the 128-token prompt in the decode leg")
     p.add_argument("--random-weights", action="store_true",
                    help="uniformly random index bytes and codebooks instead of quantized "
                         "N(0, 0.02) weights (same kernels and bytes; for profiled runs, where "
@@ -176,7 +178,12 @@ def _settle(fn, seconds=SETTLE_S, cap=20000):
 def graph_time(run, steps, warmup, settle_s=SETTLE_S, info=None):
     """Captures run() once in a HIP graph; returns ms per replay over
     `steps` timed replays, after `settle_s` seconds of untimed replays and
-    `warmup` untimed replays (see SETTLE_S)."""
+    `warmup` untimed replays (see SETTLE_S).
+
+    One step per replay, not many steps captured back to back: the
+    headline kernel streams HBM at the power limit, and without the few
+    microseconds between replays the same launches run ~7 % slower (a
+    20-launch chain measured 217.8 us per step against 210.4)."""
     run()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -367,7 +374,7 @@ def event_time(fn, reps, warmup=3, settle_s=SETTLE_S):
     return s.elapsed_time(e) / reps
 
 
-def bench_decode(dev):
+def bench_decode(dev, n_gen=256):
     """Config 4b: greedy decode tokens/s of a random-init 2.2B packed model
     (one HIP graph of launches replayed per token)."""
     from nativebit_amd.decode import DecodeEngine
@@ -375,20 +382,21 @@ def bench_decode(dev):
     cfg = ModelConfig(vocab_size=32000)
     t0 = time.time()
     model = random_packed_model(cfg, seed=0, device=dev)
-    eng = DecodeEngine(model, max_steps=512)
+    eng = DecodeEngine(model, max_steps=128 + max(n_gen, 2))
     gen = torch.Generator().manual_seed(2024)
     prompt = torch.randint(0, cfg.vocab_size, (128,), generator=gen).tolist()
-    r = eng.benchmark(prompt, 256, n_runs=3)
+    n_gen = max(n_gen, 2)
+    r = eng.benchmark(prompt, n_gen, n_runs=3)
     out = {"tokens_per_s": round(r["generate_tps"], 1), "ms_per_token": round(r["per_token_ms"], 4),
            "prompt_ms": round(r["prompt_ms"], 3), "prompt_tokens_per_s": round(r["prompt_tps"], 1),
-           "prompt_tokens": 128, "generated_tokens": 256, "vocab": cfg.vocab_size,
+           "prompt_tokens": 128, "generated_tokens": n_gen, "vocab": cfg.vocab_size,
            "runs": r["runs"], "model_build_s": round(time.time() - t0, 1),
            "engine": "DecodeEngine: the prompt as one batched pass (packed MFMA GEMMs over the "
                      "128 rows, row kernels for norms / RoPE / causal attention), then one HIP "
                      "graph of the step's launches replayed per token",
            "method": "median of 3 runs; each: the prompt pass timed on its own (prompt_ms, "
-                     "which also chooses the first generated token), then 255 graph replays "
-                     "timed (tokens_per_s)"}
+                     f"which also chooses the first generated token), then {n_gen - 1} graph "
+                     "replays timed (tokens_per_s)"}
     del eng, model
     torch.cuda.empty_cache()
     return out
@@ -761,7 +769,7 @@ def main():
         extra = {}
         wanted_extra = [e for e in args.extra.split(",") if e]
         for name, fn in (("config0", lambda: bench_config0(dev, not args.no_cpu_baseline)),
-                         ("decode", lambda: bench_decode(dev)),
+                         ("decode", lambda: bench_decode(dev, args.decode_tokens)),
                          ("prefill", lambda: bench_prefill(dev, args.random_weights)),
                          ("skinny", lambda: bench_skinny(dev, layers)),
                          ("sweep", lambda: bench_sweep(dev)),
