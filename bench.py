@@ -346,6 +346,7 @@ def cpu_baseline(mats, reps, seconds):
         once()
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
+    dec = cpu_decode_sample(t, seconds=min(6.0, seconds / 2))
     return {
         "value": round(nbytes / t / 1e9, 3), "unit": "GB/s", "cores": h["threads"], "kind": "port",
         "sample": (f"layer 0 of config 1 (q, k, v, o, gate, up, down; {nbytes} B): torch CPU "
@@ -354,6 +355,59 @@ def cpu_baseline(mats, reps, seconds):
                    f"= {t*1e3:.1f} ms per pass; {_host_desc(h)}"),
         "seconds_per_sample": round(t, 4),
         "host": h,
+        "decode_tokens_per_s": dec["tokens_per_s"],
+        "decode_sample": dec["sample"],
+    }
+
+
+def cpu_decode_sample(t_layer_linears, seconds=6.0, pos=256):
+    """Config 4b's greedy decode on the CPU, layer-bounded: one token's cost
+    = 26 x (the packed linears of one layer, timed above by cpu_baseline,
+    + that layer's two RMSNorms and its attention over `pos` cached
+    positions) + the final norm, the tied fp32 head 30 tanh(l / 30) over
+    32000 rows and the argmax -- the reference's CPU module path
+    (generate_torch.py:29-162, 298-313) with its fallback packed linear
+    (triton_kernel.py:258-275), timed piece by piece on this host."""
+    C, H, D, V, L = 2560, 20, 128, 32000, 26
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 1, C, generator=g)
+    w = torch.ones(C)
+    q = torch.randn(1, H, 1, D, generator=g)
+    kc = torch.randn(1, H, pos + 1, D, generator=g)
+    vc = torch.randn(1, H, pos + 1, D, generator=g)
+    emb = torch.randn(V, C, generator=g) * 0.02
+
+    def norm(v):
+        return v / torch.sqrt(v.pow(2).mean(-1, keepdim=True) + 1e-6) * w
+
+    def layer_rest():
+        norm(x)
+        norm(x)
+        att = (q * D ** -0.5) @ kc.transpose(-1, -2)
+        (torch.softmax(att, dim=-1) @ vc).transpose(1, 2).reshape(1, 1, C)
+
+    def head():
+        logits = 30.0 * torch.tanh((norm(x) @ emb.t()) / 30.0)
+        return int(logits[0, -1].argmax())
+
+    def timed(fn, budget):
+        fn()
+        ts, t_start = [], time.perf_counter()
+        while len(ts) < 5 or time.perf_counter() - t_start < budget:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), len(ts)
+
+    t_rest, n_rest = timed(layer_rest, seconds / 3)
+    t_head, n_head = timed(head, seconds / 3)
+    t_tok = L * (t_layer_linears + t_rest) + t_head
+    return {
+        "tokens_per_s": round(1.0 / t_tok, 3),
+        "sample": (f"{L} x (one layer's packed linears {t_layer_linears*1e3:.1f} ms + its norms and "
+                   f"attention over {pos} positions {t_rest*1e3:.2f} ms, median of {n_rest}) + "
+                   f"final norm, tied fp32 head over {V} rows and argmax {t_head*1e3:.1f} ms "
+                   f"(median of {n_head}) = {t_tok*1e3:.0f} ms per token"),
     }
 
 
