@@ -702,16 +702,8 @@ extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed
     if (!aligned(y, dtype_size(y_dtype))) return fail(NB_EALIGN, "%s: y not aligned to its dtype", fn);
     int st = ensure_device();
     if (st) return st;
-    // The 256-output-tile kernel where its grid fills the GPU (many tokens),
-    // the 128 x 128 kernel where that gives it several times more workgroups
-    // (measured on MI355X over the 2.2B shapes at M = 512 and 2048).
-    const int64_t big_tiles = (int64_t)((N + 255) / 256) * ((M + 127) / 128);
-    if (M >= 1024 || big_tiles * 4 >= (int64_t)device_cu_count() * 3) {
-        return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
-                               static_cast<hipStream_t>(stream));
-    }
-    return launch_prefill(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
-                          static_cast<hipStream_t>(stream));
+    return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
+                           static_cast<hipStream_t>(stream));
 }
 
 extern "C" int64_t nb_gemm_prefill_ws_bytes(int M, int N, int K) {

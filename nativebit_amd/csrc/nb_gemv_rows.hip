@@ -168,7 +168,21 @@ void gemv_rows_kernel(RowsArgs a) {
     //         form them in fp32, round to bf16, stage in the selector layout
     wait_vm_n<SLOTS * kLoads>(early * kLoads);
     for (int i = early; i < first; ++i) issue(c0 + wave + i * kWaves, i);
-    __syncthreads();  // every wave's pieces are in LDS
+    typedef __attribute__((ext_vector_type(4))) float f4;
+    if constexpr (XMODE == NB_X_RMSNORM) {
+        // the norm's sum of squares over this wave's own pieces of x (in LDS
+        // now), so that one barrier publishes both the pieces and the sums
+        const f4* xr4 = reinterpret_cast<const f4*>(raw);
+        float ssw = 0.f;
+        for (int p = wave; p * 1024 < 4 * K; p += kWaves) {
+            const int e0 = p * 256 + 4 * lane;   // K % 4 == 0: a lane's 4 are all in or out
+            const f4 v = xr4[e0 >> 2];
+            if (e0 < K) ssw += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+        }
+        ssw = wsum(ssw);
+        if (lane == 0) red[wave] = ssw;
+    }
+    __syncthreads();  // every wave's pieces (and partial sums) are in LDS
     const int ng = K >> 3;
     constexpr int kMaxG = (kMaxK / 8 + kThreads - 1) / kThreads;
     uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
@@ -185,11 +199,9 @@ void gemv_rows_kernel(RowsArgs a) {
         }
     } else {
         // each thread's groups of 8 inputs, read once into registers
-        typedef __attribute__((ext_vector_type(4))) float f4;
         const f4* xf4 = reinterpret_cast<const f4*>(raw);
         const f4* sf4 = reinterpret_cast<const f4*>(raw + a.raw_bytes / 2);
         f4 xr[kMaxG][2], sr[kMaxG][2];
-        float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < kMaxG; ++j) {
             const int g = tid + j * kThreads;
@@ -198,18 +210,9 @@ void gemv_rows_kernel(RowsArgs a) {
             xr[j][1] = xf4[2 * gg + 1];
             sr[j][0] = sf4[2 * gg];
             sr[j][1] = sf4[2 * gg + 1];
-            if (XMODE == NB_X_RMSNORM && g < ng) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-                    ss += xr[j][h].x * xr[j][h].x + xr[j][h].y * xr[j][h].y +
-                          xr[j][h].z * xr[j][h].z + xr[j][h].w * xr[j][h].w;
-            }
         }
         float norm = 1.f;
         if constexpr (XMODE == NB_X_RMSNORM) {
-            ss = wsum(ss);
-            if (lane == 0) red[wave] = ss;
-            __syncthreads();
             float t = 0.f;
             for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
             norm = sqrtf(t / (float)K + a.eps);

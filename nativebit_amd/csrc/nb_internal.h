@@ -116,11 +116,8 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
                    int n_entries, int block_size, hipStream_t stream);
 
 
-// Prefill GEMM with a packed weight (nb_prefill.hip); arguments validated.
-int launch_prefill(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
-                   void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
-
-// The same contraction with 256-output x 256/128-token tiles (nb_prefill2.hip).
+// Prefill GEMM with a packed weight (nb_prefill2.hip): the packed weight
+// dequantized into LDS tiles, bf16 MFMAs; arguments validated.
 int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
                     void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
 

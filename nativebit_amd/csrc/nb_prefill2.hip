@@ -5,7 +5,8 @@
 // The reference computes this as unpack + gather + a dense matmul that
 // materialises W on every call (inference/triton_kernel.py:258-275; in bf16,
 // inference/eval_ppl.py:149-174).  Here a 512-thread workgroup owns a BN x
-// BM tile of Y^T (BN outputs x BM tokens) and walks K in steps of 64:
+// BM tile of Y^T (BN = 256 or 128 outputs x BM = 256, 128 or 64 tokens,
+// chosen per launch by grid occupancy) and walks K in steps of 64:
 //
 //   * the X slice (BM tokens x 64 bf16) arrives by global_load_lds_dwordx4
 //     (eight rows per instruction), 16-byte chunk c of row r in LDS slot
@@ -312,20 +313,31 @@ int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const flo
     a.M = M;
     a.N = N;
     a.K = K;
-    constexpr int BN = 256;
     constexpr int W = NB_PREFILL_WAVES;
-    const int gn = (N + BN - 1) / BN;
-    // 256-token tiles when they give the CUs enough workgroups, else 128
-    const int cus = device_cu_count();
-    if ((int64_t)gn * ((M + 255) / 256) >= (int64_t)cus * 3 / 4) {
-        const size_t lds = 2 * (256 + BN) * kRowBytes;
-        hipLaunchKernelGGL((prefill2_kernel<256, BN, W>), dim3(gn, (M + 255) / 256),
-                           dim3(64 * W), lds, stream, a);
+    // The largest tile (fewest workgroups, least redundant traffic) whose
+    // grid still gives about 0.6 workgroups per CU; where none does (few
+    // tokens, narrow layers), the smallest, for the most workgroups.
+    // (Measured on MI355X over the four 2.2B layer shapes at M = 128, 512
+    // and 2048: this choice was the fastest tile, or within 1 % of it, in
+    // all twelve cases.)
+    const int64_t want = (int64_t)device_cu_count() * 3 / 5;
+    auto groups = [&](int bm, int bn) {
+        return (int64_t)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
+    };
+#define NB_PREFILL2_LAUNCH(BMv, BNv)                                                          \
+    hipLaunchKernelGGL((prefill2_kernel<BMv, BNv, W>),                                      \
+                       dim3((N + BNv - 1) / BNv, (M + BMv - 1) / BMv), dim3(64 * W),          \
+                       (size_t)2 * (BMv + BNv) * kRowBytes, stream, a)
+    if (groups(256, 256) >= want) {
+        NB_PREFILL2_LAUNCH(256, 256);
+    } else if (groups(256, 128) >= want) {
+        NB_PREFILL2_LAUNCH(256, 128);
+    } else if (groups(128, 128) >= want) {
+        NB_PREFILL2_LAUNCH(128, 128);
     } else {
-        const size_t lds = 2 * (128 + BN) * kRowBytes;
-        hipLaunchKernelGGL((prefill2_kernel<128, BN, W>), dim3(gn, (M + 127) / 128),
-                           dim3(64 * W), lds, stream, a);
+        NB_PREFILL2_LAUNCH(64, 128);
     }
+#undef NB_PREFILL2_LAUNCH
     return check_launch("nb_gemm_prefill");
 }
 
