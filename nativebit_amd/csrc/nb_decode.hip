@@ -409,26 +409,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step2_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// attention in 256-position tiles, head_dim 128 (the decode model's shape)
+// attention in TP-position tiles, head_dim 128 (the decode model's shape)
 // ---------------------------------------------------------------------------
-// Workgroup (hd, s) of 512 threads takes positions [256 s, 256 s + 256) of
-// head hd; only ceil((pos + 1) / 256) tiles are in use, so up to 256 cached
-// positions a head is one workgroup and no split combine runs at all.  All
-// global loads are issued before the first is used, as 16-byte loads (32
-// per thread): keys as (4 positions x 16 dimensions) per thread, values as
-// (16 positions x 4 dimensions), so one memory latency and the tile's bytes
-// bound the launch.  Scores: 8 partial sums over 16 dimensions, added in
-// order; softmax partials per wave of 64 positions (max, sum of exp); the
-// weighted values per group of 16 positions, merged in group order with the
-// waves' factors exp(m_w - M).  With more than one tile in use, each writes
-// (M, L, O) and the last to finish (agent-scope counter) merges them as
-// attention_step2_kernel does.  Keys [n_head][128][ctx] and values
-// [n_head][ctx][128] fp32, ctx % 4 == 0, 16-byte aligned.
+// Workgroup (hd, s) of 512 threads takes positions [TP s, TP s + TP) of head
+// hd; only ceil((pos + 1) / TP) tiles are in use.  All global loads are
+// issued before the first is used, as 16-byte loads: keys as (4 positions x
+// DPG dimensions) per thread, values as (PPG positions x 4 dimensions), so
+// one memory latency and the tile's bytes bound the launch.  Scores: DG
+// partial sums over DPG dimensions, added in order; softmax partials per
+// wave of 64 positions (max, sum of exp); the weighted values per group of
+// PPG positions, merged in group order with the waves' factors exp(m_w -
+// M).  With more than one tile in use, each writes (M, L, O) and the last to
+// finish (agent-scope counter) merges them in tile order.  Keys
+// [n_head][128][ctx] and values [n_head][ctx][128] fp32, ctx % 4 == 0,
+// 16-byte aligned.
 constexpr int kTileD = 128;
-constexpr int kTilePos = 256;
 constexpr int kTileThreads = 512;
-static_assert(kTilePos * 4 >= kMaxCtx, "tiles cover the context");
+#ifndef NB_ATT_TILE
+#define NB_ATT_TILE 128
+#endif
+constexpr int kTilePos = NB_ATT_TILE;
+static_assert(kMaxCtx / kTilePos <= kAttnSplits, "tiles fit the partials buffer");
 
+template <int TP>
 __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     const float* __restrict__ qkv, float* __restrict__ k_cache, float* __restrict__ v_cache,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t,
@@ -436,20 +439,27 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     void* __restrict__ out, int out_dtype, int n_head, int ctx) {
     typedef __attribute__((ext_vector_type(4))) float f4;
     constexpr int D = kTileD;
+    constexpr int PQ = TP / 4;                 // key position quads
+    constexpr int DG = kTileThreads / PQ;      // key dimension groups
+    constexpr int DPG = D / DG;                // dimensions per group
+    constexpr int G = kTileThreads / (D / 4);  // value position groups (16)
+    constexpr int PPG = TP / G;                // positions per value group
+    constexpr int NW = TP / 64;                // softmax waves
+    static_assert(DPG % 4 == 0 && PPG % 4 == 0 && NW >= 1, "tile shape");
     __shared__ __align__(16) float qs[D], kn[D], vn[D];
-    __shared__ __align__(16) float sc[8][kTilePos];
-    __shared__ __align__(16) float pl[kTilePos];
-    __shared__ __align__(16) float oh[16][D];
-    __shared__ float wm[4], wl[4];
+    __shared__ __align__(16) float sc[DG][TP];
+    __shared__ __align__(16) float pl[TP];
+    __shared__ __align__(16) float oh[G][D];
+    __shared__ float wm[NW], wl[NW];
     __shared__ unsigned last;
     const int hd = blockIdx.x, s = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int pos = st->pos;
     if (pos < 0 || pos >= ctx) return;  // past the cache: nothing to do
     const int n = pos + 1;
-    const int S = (n + kTilePos - 1) / kTilePos;  // tiles in use
+    const int S = (n + TP - 1) / TP;  // tiles in use
     if (s >= S) return;
-    const int t0 = s * kTilePos, len = min(kTilePos, n - t0);
+    const int t0 = s * TP, len = min(TP, n - t0);
     const int C = n_head * D;
     const float scale = 1.0f / sqrtf((float)D);
 
@@ -465,19 +475,19 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
         sn = sin_t[(int64_t)pos * (D / 2) + tid];
     }
     if (tid < D) v0 = qkv[2 * C + hd * D + tid];
-    const int pq = tid & 63, dg = wave;                  // keys: 4 positions, 16 dims
+    const int pq = tid % PQ, dg = tid / PQ;           // keys: 4 positions, DPG dims
     const int tk = t0 + min(4 * pq, (len - 1) & ~3);
     const float* kt = k_cache + (int64_t)hd * D * ctx;
-    f4 kr[16];
+    f4 kr[DPG];
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-        kr[j] = *reinterpret_cast<const f4*>(kt + (int64_t)(16 * dg + j) * ctx + tk);
-    const int dq = tid & 31, g = tid >> 5;               // values: 16 positions, 4 dims
+    for (int j = 0; j < DPG; ++j)
+        kr[j] = *reinterpret_cast<const f4*>(kt + (int64_t)(DPG * dg + j) * ctx + tk);
+    const int dq = tid & 31, g = tid >> 5;               // values: PPG positions, 4 dims
     const float* vc = v_cache + (int64_t)hd * ctx * D;
-    f4 vr[16];
+    f4 vr[PPG];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-        const int tt = t0 + min(16 * g + j, len - 1);
+    for (int j = 0; j < PPG; ++j) {
+        const int tt = t0 + min(PPG * g + j, len - 1);
         vr[j] = *reinterpret_cast<const f4*>(vc + (int64_t)tt * D + 4 * dq);
     }
 
@@ -498,8 +508,8 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     if (pos >= tk && pos < tk + 4) {
         const int i = pos - tk;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float v = kn[16 * dg + j];
+        for (int j = 0; j < DPG; ++j) {
+            const float v = kn[DPG * dg + j];
             kr[j].x = i == 0 ? v : kr[j].x;
             kr[j].y = i == 1 ? v : kr[j].y;
             kr[j].z = i == 2 ? v : kr[j].z;
@@ -509,17 +519,17 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     if (s == S - 1) {  // (positions past the tile's end were read as pos too)
         const f4 nv = *reinterpret_cast<const f4*>(vn + 4 * dq);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            if (t0 + min(16 * g + j, len - 1) == pos) vr[j] = nv;
+        for (int j = 0; j < PPG; ++j) {
+            if (t0 + min(PPG * g + j, len - 1) == pos) vr[j] = nv;
         }
     }
 
-    // ---- scores: this thread's 4 positions over its 16 dimensions
+    // ---- scores: this thread's 4 positions over its DPG dimensions
     {
         f4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4) {
-            const f4 qv = *reinterpret_cast<const f4*>(qs + 16 * dg + 4 * j4);
+        for (int j4 = 0; j4 < DPG / 4; ++j4) {
+            const f4 qv = *reinterpret_cast<const f4*>(qs + DPG * dg + 4 * j4);
             acc += qv.x * kr[4 * j4];
             acc += qv.y * kr[4 * j4 + 1];
             acc += qv.z * kr[4 * j4 + 2];
@@ -528,12 +538,12 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
         *reinterpret_cast<f4*>(&sc[dg][4 * pq]) = acc;
     }
     __syncthreads();
-    if (wave < 4) {  // position tid: its score, the wave's max and sum of exp
+    if (wave < NW) {  // position tid: its score, the wave's max and sum of exp
         float sv = -INFINITY;
         if (tid < len) {
             sv = 0.f;
 #pragma unroll
-            for (int k = 0; k < 8; ++k) sv += sc[k][tid];
+            for (int k = 0; k < DG; ++k) sv += sc[k][tid];
         }
         const float m = wave_max(sv);
         const float e = tid < len ? __expf(sv - m) : 0.f;
@@ -545,12 +555,12 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
         }
     }
     __syncthreads();
-    // ---- weighted values of this thread's 16 positions, 4 dimensions
+    // ---- weighted values of this thread's PPG positions, 4 dimensions
     {
         f4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j4 = 0; j4 < 4; ++j4) {
-            const f4 pv = *reinterpret_cast<const f4*>(pl + 16 * g + 4 * j4);
+        for (int j4 = 0; j4 < PPG / 4; ++j4) {
+            const f4 pv = *reinterpret_cast<const f4*>(pl + PPG * g + 4 * j4);
             o += pv.x * vr[4 * j4];
             o += pv.y * vr[4 * j4 + 1];
             o += pv.z * vr[4 * j4 + 2];
@@ -563,16 +573,16 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     if (tid < D) {
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, wm[w]);
-        float f[4], L = 0.f;
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, wm[w]);
+        float f[NW], L = 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NW; ++w) {
             f[w] = wm[w] == -INFINITY ? 0.f : __expf(wm[w] - M);
             L += f[w] * wl[w];
         }
         float O = 0.f;
 #pragma unroll
-        for (int gg = 0; gg < 16; ++gg) O += f[gg >> 2] * oh[gg][tid];
+        for (int gg = 0; gg < G; ++gg) O += f[(gg * PPG) / 64] * oh[gg][tid];
         if (S == 1) {
             store_act(out, out_dtype, hd * D + tid, O / L);
         } else {
@@ -595,12 +605,13 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
     }
     __syncthreads();
     if (!last) return;
+    constexpr int kT = kMaxCtx / TP;  // tiles a head can have
     const float* base = work + (int64_t)hd * kAttnSplits * (kMaxHeadDim + 2);
     if (tid < D) {
-        float mj[4], lj[4], oj[4];
+        float mj[kT], lj[kT], oj[kT];
         float M = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kT; ++j) {
             const float* pj = base + j * (kMaxHeadDim + 2);
             mj[j] = j < S ? get_agent(pj) : -INFINITY;
             lj[j] = j < S ? get_agent(pj + 1) : 0.f;
@@ -609,7 +620,7 @@ __global__ __launch_bounds__(kTileThreads) void attention_tile_kernel(
         }
         float L = 0.f, O = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < kT; ++j) {
             const float fj = mj[j] == -INFINITY ? 0.f : __expf(mj[j] - M);
             L += fj * lj[j];
             O += fj * oj[j];
@@ -808,7 +819,7 @@ int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, cons
                           int ctx, hipStream_t stream) {
     if (head_dim == kTileD && ctx % 4 == 0 && reinterpret_cast<uintptr_t>(k_cache) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(v_cache) % 16 == 0) {
-        hipLaunchKernelGGL(attention_tile_kernel, dim3(n_head, kMaxCtx / kTilePos),
+        hipLaunchKernelGGL(attention_tile_kernel<kTilePos>, dim3(n_head, kMaxCtx / kTilePos),
                            dim3(kTileThreads), 0, stream, qkv, k_cache, v_cache, cos_t, sin_t, st,
                            work, done, out, out_dtype, n_head, ctx);
     } else if (head_dim <= kAttn2MaxD) {
