@@ -908,6 +908,10 @@ void decode_persistent_kernel(PArgs args) {
     wait_vm<0>();  // no ring load outlives the workgroup
 }
 
+__global__ void clear_ctl_kernel(unsigned* __restrict__ ctl, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ctl[i] = 0u;
+}
+
 }  // namespace
 
 int64_t decode_persistent_workspace_bytes(int C, int H, int F) {
@@ -996,10 +1000,11 @@ int launch_decode_persistent(const nb_decode_model& m, void* workspace, nb_decod
     a.n_steps = n_steps;
     a.eps = m.eps;
     a.spin_limit = spin_limit;
-    // barrier counters, error word and split counters start at zero
-    if (hipMemsetAsync(ws, 0, kCtlBytes, stream) != hipSuccess) {
-        return fail(NB_ELAUNCH, "nb_decode_persistent: clearing the control block failed");
-    }
+    // barrier counters, error word and split counters start at zero (a
+    // kernel, not a memset node: the call stays graph-capturable)
+    hipLaunchKernelGGL(clear_ctl_kernel, dim3(1), dim3(256), 0, stream,
+                       reinterpret_cast<unsigned*>(ws), kCtlBytes / 4);
+    if (check_launch("nb_decode_persistent") != NB_OK) return NB_ELAUNCH;
     void* args[] = {&a};
     const hipError_t e = hipLaunchCooperativeKernel((const void*)decode_persistent_kernel, dim3(G),
                                                     dim3(kThreads), args, kLdsBytes, stream);

@@ -24,7 +24,10 @@
 //   * two LDS stages and one barrier per step: while a step's MFMAs run, the
 //     next step's X slice is in flight and its W slice is dequantized, and
 //     the two waves of each SIMD overlap one's MFMAs with the other's
-//     dequantization and LDS reads.
+//     dequantization and LDS reads;
+//   * a one-dimensional grid whose workgroups (dealt to the 8 XCDs in turn)
+//     take tiles XCD by XCD in contiguous runs, so an XCD's L2 holds the X
+//     tiles of one or two token blocks rather than of all of them.
 // Weights are the codebook entries rounded to bf16 (RNE), as the bf16 path;
 // accumulation is fp32.
 #include <algorithm>
@@ -134,7 +137,18 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     using WR = WRegs<H>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs in turn
+    // (workgroup g to XCD g % 8), each XCD with its own L2: XCD x takes a
+    // contiguous run of the tiles in (token tile, output tile) order, so
+    // its workgroups share one or two token tiles of X in its L2 rather
+    // than all of them.
+    const int nn = (a.N + BN - 1) / BN;
+    int tile;
+    {
+        const int T = gridDim.x, g = blockIdx.x, full = T / 8, rem = T % 8, x = g % 8;
+        tile = x * full + min(x, rem) + g / 8;
+    }
+    const int n0 = (tile % nn) * BN, m0 = (tile / nn) * BM;
     const int bpr = a.K / 128;
     const int nsteps = a.K / kBK;
     const uint32_t base = lds_addr(smem);
@@ -326,7 +340,7 @@ int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const flo
     };
 #define NB_PREFILL2_LAUNCH(BMv, BNv)                                                          \
     hipLaunchKernelGGL((prefill2_kernel<BMv, BNv, W>),                                      \
-                       dim3((N + BNv - 1) / BNv, (M + BMv - 1) / BMv), dim3(64 * W),          \
+                       dim3((unsigned)groups(BMv, BNv)), dim3(64 * W),                       \
                        (size_t)2 * (BMv + BNv) * kRowBytes, stream, a)
     if (groups(256, 256) >= want) {
         NB_PREFILL2_LAUNCH(256, 256);
