@@ -714,6 +714,37 @@ def test_skinny_batched_more_items_than_one_launch(dev):
     assert all(torch.isfinite(it[3]).all().item() for it in items)
 
 
+@pytest.mark.parametrize("M", [5, 14])
+def test_skinny_batched_task_runs_cross_items(dev, M):
+    """Workgroups walk contiguous task runs that cross item boundaries (here
+    every workgroup holds several small items, some with a partial last
+    slice and ragged rows), with three x buffers (M <= 13) or two; every item
+    equals the fp64 brute force, and a y += item adds."""
+    n = 400
+    items, refs = [], []
+    for i in range(n):
+        N, K = 1 + (i * 53) % 300, 128 * (1 + i % 7)
+        idx, p, cb = random_layer(N, K, 3, 8, 128, 7000 + i)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(900 + i)).to(torch.bfloat16)
+        y0 = torch.randn(M, N, generator=torch.Generator().manual_seed(5 + i))
+        add = i % 5 == 0
+        y = (y0.clone() if add else torch.full((M, N), float("nan"))).to(dev)
+        item = (x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), y, N, K)
+        items.append(item + (({"y": "add"},) if add else ()))
+        refs.append((idx, cb, x, y0 if add else None))
+    note(f"skinny M={M} with {n} small items")
+    ops.GemvBatch(items, m=M).run()
+    torch.cuda.synchronize()
+    for i in range(0, n, 3):
+        idx, cb, x, y0 = refs[i]
+        N, K = items[i][4], items[i][5]
+        ref = ref_gemv(x, idx, cb, 128, N, K)
+        got = items[i][3].cpu()
+        if y0 is not None:
+            got = got - y0  # (an overwrite instead of an add would leave -y0 here)
+        assert rel(got, ref) <= REL_F32, (i, N, K, y0 is not None)
+
+
 def test_batched_add_twice_accumulates(dev):
     """y_mode add reads y each launch: two runs add the product twice."""
     N, K = 2560, 2560
@@ -731,7 +762,7 @@ def test_batched_add_twice_accumulates(dev):
     assert rel((y - y0).cpu(), (2 * yp).cpu()) <= 1e-5
 
 
-@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 8, 13, 14, 16])
 def test_skinny_batched_vs_f64(dev, M):
     """nb_gemm_skinny_batched over mixed shapes (ragged N, K with a partial
     last 512-slice, an empty item) equals the fp64 brute force on the
