@@ -126,8 +126,9 @@ def test_attention_step(dev, H, D, ctx):
     done = torch.zeros(H, dtype=torch.int32, device=dev)
     kd, vd = kc.transpose(1, 2).contiguous().to(dev), vc.to(dev)   # keys [H][D][ctx]
     cosd, sind = cos.to(dev), sin.to(dev)
-    for pos in sorted(p for p in {0, 1, 15, 16, 17, 63, 255, 256, 257, 511, 767, 768, ctx // 2,
-                                  ctx - 1} if p < ctx):
+    # (tile edges of the 128-position tile kernel and of the 16-split kernels)
+    for pos in sorted(p for p in {0, 1, 15, 16, 17, 63, 127, 128, 129, 255, 256, 257, 383, 384,
+                                  511, 767, 768, 895, 896, ctx // 2, ctx - 1} if p < ctx):
         note(f"attention H={H} D={D} pos={pos}")
         qkv = torch.randn(3 * H * D, generator=g)
         qkvd = qkv.to(dev)

@@ -816,15 +816,18 @@ def test_skinny_batched_forms(dev):
         assert rel(y32[m].cpu(), ops.gemv(x[m].contiguous(), pt, ct, N, K).cpu()) <= 1e-5
 
 
-def test_batched_graph_replay(dev):
+@pytest.mark.parametrize("M", [1, 4])
+def test_batched_graph_replay(dev, M):
     """Captured in a HIP graph and replayed several times, with eager work in
-    between, every replay reproduces the eager result."""
+    between, every replay reproduces the eager result (M = 1: the streaming
+    kernel; M = 4: the skinny kernel)."""
     N, K = 2560, 2560
     idx, p, cb = random_layer(N, K, 3, 8, 128, 4242)
     pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
-    x = torch.randn(K, device=dev).to(torch.bfloat16)
-    y = torch.empty(N, device=dev)
-    b = ops.GemvBatch([(x, pt, ct, y, N, K)])
+    x = torch.randn(K, device=dev).to(torch.bfloat16) if M == 1 else \
+        torch.randn(M, K, device=dev).to(torch.bfloat16)
+    y = torch.empty(N, device=dev) if M == 1 else torch.empty(M, N, device=dev)
+    b = ops.GemvBatch([(x, pt, ct, y, N, K)], m=M)
     b.run()
     torch.cuda.synchronize()
     eager = y.clone()
