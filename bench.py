@@ -516,10 +516,16 @@ def bench_skinny(dev, layers):
     """Config 2: M activation rows over all 182 matmuls of a step.
 
     batched: one launch per step -- nb_gemv_batched (the streaming kernel)
-    at M = 1, nb_gemm_skinny_batched at M > 1 -- replayed as a HIP graph;
-    per_matmul: 182 nb_gemv launches per step (one per matmul) in a graph."""
+    at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2..4
+    (the layers re-ordered once by nb_quad_layout, outside the timing, as
+    at model load), nb_gemm_skinny_batched at M > 4 -- replayed as a HIP
+    graph; rows_layout: nb_gemm_skinny_batched on the original layout, for
+    comparison; per_matmul: 182 nb_gemv launches per step (one per matmul)
+    in a graph."""
     from nativebit_amd import ops, synth
     mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
+    quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats]
+    torch.cuda.synchronize()
     out = {}
     for M in (1, 2, 4, 8, 16):
         xs = {K: synth.make_activation(K, m=M, seed=M, device=dev, dtype=torch.bfloat16)
@@ -530,7 +536,21 @@ def bench_skinny(dev, layers):
         batch = ops.GemvBatch([((xs[m.K][0] if M == 1 else xs[m.K]), m.packed, m.cb,
                                 (y[0] if M == 1 else y), m.N, m.K) for m, y in zip(mats, ys)],
                               m=M)
-        ms_b = graph_time(batch.run, 20, 5)
+        ms_rows = graph_time(batch.run, 20, 5)
+        ms_b, kernel = ms_rows, "gemv_stream_kernel" if M == 1 else "gemv_skinny_kernel"
+        extra = {}
+        if 2 <= M <= 4:
+            yq = [torch.empty(M, m.N, device=dev) for m in mats]
+            qbatch = ops.GemvBatch([(xs[m.K], q[0], q[1], y, m.N, m.K)
+                                    for m, q, y in zip(mats, quads, yq)], m=M, layout="quad")
+            ms_b, kernel = graph_time(qbatch.run, 20, 5), "gemv_quad_kernel"
+            # the two kernels' products agree (fp32 sums in different orders)
+            worst = max(float((a - b).norm() / b.norm()) for a, b in zip(yq[:7], ys[:7]))
+            if worst > 1e-5:
+                raise RuntimeError(f"skinny M={M}: quad and row layouts disagree ({worst:.2e})")
+            extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
+                     "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
+            del yq, qbatch
 
         def run():
             for m, y in zip(mats, ys):
@@ -538,15 +558,17 @@ def bench_skinny(dev, layers):
         ms_p = graph_time(run, 20, 5)
         out[f"M{M}"] = {"us_per_step": round(ms_b * 1e3, 1), "GB_s": round(nbytes / ms_b / 1e6, 1),
                         "pct_hbm_peak": round(nbytes / ms_b / 1e6 / HBM_PEAK_GBS * 100, 1),
-                        "TFLOP_s": round(fl / ms_b / 1e9, 2),
-                        "kernel": "gemv_stream_kernel" if M == 1 else "gemv_skinny_kernel",
+                        "TFLOP_s": round(fl / ms_b / 1e9, 2), "kernel": kernel, **extra,
                         "per_matmul_us_per_step": round(ms_p * 1e3, 1),
                         "per_matmul_GB_s": round(nbytes / ms_p / 1e6, 1)}
-        log(f"[bench] skinny M={M}: batched {ms_b*1e3:.1f} us ({nbytes/ms_b/1e6:.0f} GB/s), "
-            f"per-matmul launches {ms_p*1e3:.1f} us")
+        log(f"[bench] skinny M={M}: batched {ms_b*1e3:.1f} us ({nbytes/ms_b/1e6:.0f} GB/s, "
+            f"{kernel}), per-matmul launches {ms_p*1e3:.1f} us")
         del ys, xs, batch
-    out["note"] = ("batched: every matmul of the step in one launch (graph replay); "
-                   "per_matmul: 182 nb_gemv launches per step in one graph")
+    out["note"] = ("batched: every matmul of the step in one launch (graph replay); M = 2..4 "
+                   "on the row-quad layout (nb_quad_layout, once, untimed), rows_layout the "
+                   "same products on the original layout; per_matmul: 182 nb_gemv launches "
+                   "per step in one graph")
+    del quads
     return out
 
 

@@ -262,6 +262,32 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
 int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count,
                            int M, int y_dtype, void* stream);
 
+/* Row-quad layout of a 3-bit / 8-entry / block-128 N x K layer: the same
+ * 128-weight blocks (48 index bytes, 8 fp32 codebook entries each) with the
+ * rows taken four at a time (N rounded up to a multiple of 4 with zero
+ * blocks) and the four rows' blocks of one column block side by side:
+ *     block 4 (q * K/128 + kb) + i  =  row 4q + i, column block kb.
+ * qpacked holds nb_quad_layout_bytes(N, K) bytes, qcodebook
+ * nb_quad_layout_bytes(N, K) * 2 / 3 bytes (ceil(N/4) * 4 * K/128 * 8
+ * floats); both 16-byte aligned, as packed and codebook.
+ * No counterpart in the reference: a one-time re-ordering of a layer's
+ * packed bytes (for instance at model load) for nb_gemm_skinny_quad_batched.
+ */
+int64_t nb_quad_layout_bytes(int N, int K);
+int nb_quad_layout(const uint8_t* packed, const float* codebook, int N, int K,
+                   uint8_t* qpacked, float* qcodebook, void* stream);
+
+/* nb_gemm_skinny_batched for M = 1..4 on layers in the row-quad layout:
+ * every item's packed / codebook are nb_quad_layout's output for that
+ * item's N x K (N the layer's own row count); x, y, y_mode and table_dev as
+ * for nb_gemm_skinny_batched, K >= 2048.  Replaces the same reference
+ * branch (inference/triton_kernel.py:258-275, bf16 form of inference/
+ * eval_ppl.py:149-174) for the two to four token rows of a small-batch
+ * decode step: one v_mfma_f32_4x4x4_16b_bf16 serves four rows and four
+ * tokens, so the per-weight work is that of M = 1. */
+int nb_gemm_skinny_quad_batched(const nb_batch_item* items, const void* table_dev, int count,
+                                int M, int y_dtype, void* stream);
+
 
 /* ------------------------------------------------------------------------
  * Decode step (one token, batch 1) -- the non-GEMV kernels of the packed

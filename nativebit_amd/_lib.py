@@ -62,6 +62,9 @@ SIGNATURES = {
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),
     "nb_gemm_skinny_batched": (_I, [_P, _P, _I, _I, _I, _P]),
+    "nb_quad_layout_bytes": (_L, [_I, _I]),
+    "nb_quad_layout": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "nb_gemm_skinny_quad_batched": (_I, [_P, _P, _I, _I, _I, _P]),
     "nb_gemm_prefill": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P]),
     "nb_gemm_prefill_ws_bytes": (_L, [_I, _I, _I]),
     "nb_gemm_prefill_ws": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P, _L, _P]),

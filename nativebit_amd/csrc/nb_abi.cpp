@@ -432,14 +432,21 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
                               y_dtype, static_cast<hipStream_t>(stream));
 }
 
-int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
-                           int y_dtype, void* stream) {
-    const char* fn = "nb_gemm_skinny_batched";
+}  // extern "C"
+
+namespace {
+
+// nb_gemm_skinny_batched and its row-quad form: shared validation, then
+// the kernel the layout calls for.
+int skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
+                   int y_dtype, void* stream, bool quad) {
+    const char* fn = quad ? "nb_gemm_skinny_quad_batched" : "nb_gemm_skinny_batched";
     int64_t chunks = 0;
     int mk = 0;
     int st = check_batch(items, count, fn, &chunks, &mk);
     if (st) return st;
-    if (M < 1 || M > 16) return fail(NB_EINVAL, "%s: M=%d outside 1..16", fn, M);
+    const int max_m = quad ? 4 : 16;
+    if (M < 1 || M > max_m) return fail(NB_EINVAL, "%s: M=%d outside 1..%d", fn, M, max_m);
     if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
     if (chunks == 0) return NB_OK;
     if (!table_dev) return fail(NB_EINVAL, "%s: table_dev is NULL", fn);
@@ -460,13 +467,60 @@ int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, in
         if (items[i].y_mode == NB_Y_ADD && y_dtype != NB_F32) {
             return fail(NB_EUNSUPPORTED, "%s: item %d NB_Y_ADD needs fp32 outputs", fn, i);
         }
+        if (quad && items[i].K < 2048) {
+            return fail(NB_EUNSUPPORTED, "%s: item %d K=%d (the row-quad kernel needs K >= 2048)",
+                        fn, i, items[i].K);
+        }
     }
     st = ensure_device();
     if (st) return st;
     std::vector<StreamProblem> host((size_t)nprob);
     build_stream_table(items, count, host.data());
+    if (quad) {
+        return launch_gemv_quad(static_cast<const StreamProblem*>(table_dev), host.data(), nprob,
+                                M, y_dtype, static_cast<hipStream_t>(stream));
+    }
     return launch_gemv_skinny(static_cast<const StreamProblem*>(table_dev), host.data(), nprob, M,
                               y_dtype, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
+                           int y_dtype, void* stream) {
+    return skinny_batched(items, table_dev, count, M, y_dtype, stream, false);
+}
+
+int nb_gemm_skinny_quad_batched(const nb_batch_item* items, const void* table_dev, int count,
+                                int M, int y_dtype, void* stream) {
+    return skinny_batched(items, table_dev, count, M, y_dtype, stream, true);
+}
+
+int64_t nb_quad_layout_bytes(int N, int K) {
+    if (N < 0 || K < 0 || K % 128) return 0;
+    return (int64_t)((N + 3) / 4) * 4 * (K / 128) * 48;
+}
+
+int nb_quad_layout(const uint8_t* packed, const float* codebook, int N, int K, uint8_t* qpacked,
+                   float* qcodebook, void* stream) {
+    const char* fn = "nb_quad_layout";
+    if (N < 0 || K <= 0 || K % 128 || K > 8192) {
+        return fail(NB_EINVAL, "%s: N=%d K=%d (needs K %% 128 == 0, 0 < K <= 8192)", fn, N, K);
+    }
+    if (N == 0) return NB_OK;
+    if (!packed || !codebook || !qpacked || !qcodebook) {
+        return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    }
+    if (!aligned(packed, 16) || !aligned(codebook, 16) || !aligned(qpacked, 16) ||
+        !aligned(qcodebook, 16)) {
+        return fail(NB_EALIGN, "%s: packed/codebook/qpacked/qcodebook not 16-byte aligned", fn);
+    }
+    const int st = ensure_device();
+    if (st) return st;
+    return launch_quad_layout(packed, codebook, N, K, qpacked, qcodebook,
+                              static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -97,6 +97,16 @@ int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host
 int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host_probs,
                        int nprob, int M, int y_dtype, hipStream_t stream);
 
+// The batched skinny GEMM for M <= 4 on the row-quad layout
+// (nb_gemv_quad.hip); gemv_quad_supported says whether the batch is in its
+// domain (M, K >= 2048, bf16 x, LDS).
+bool gemv_quad_supported(const StreamProblem* host_probs, int nprob, int M);
+int launch_gemv_quad(const StreamProblem* dev_probs, const StreamProblem* host_probs,
+                     int nprob, int M, int y_dtype, hipStream_t stream);
+// Writes the row-quad layout of an N x K layer.
+int launch_quad_layout(const uint8_t* packed, const float* codebook, int N, int K,
+                       uint8_t* qpacked, float* qcodebook, hipStream_t stream);
+
 // Kernel launchers (arguments already validated by nb_abi.cpp).
 int launch_gemv(const GemvArgs& a, hipStream_t stream);
 // The bf16-activation MFMA GEMV; returns 1 (launching nothing) when the

@@ -158,15 +158,24 @@ class GemvBatch:
     (m, N) matrix, both contiguous; only the plain bf16 activation form is
     available then (the output may still be "add").
 
+    ``layout="quad"`` (m <= 4, K >= 2048): every item's packed / codebook
+    are the row-quad layout of its layer (``quad_layout``), run by
+    nb_gemm_skinny_quad_batched.
+
     The device table is built once here; each run() enqueues one launch on
     torch's current stream (graph-capturable).  The tensors are referenced
     by pointer: keep them alive and in place.
     """
 
-    def __init__(self, items, m: int = 1):
+    def __init__(self, items, m: int = 1, layout: str = "rows"):
         if not 1 <= m <= 16:
             raise ValueError(f"m={m} outside 1..16")
+        if layout not in ("rows", "quad"):
+            raise ValueError(f"unknown layout {layout!r}")
+        if layout == "quad" and m > 4:
+            raise ValueError(f"the row-quad kernel takes m <= 4 (got {m})")
         self.m = int(m)
+        self.layout = layout
         self.items = list(items)
         n = len(self.items)
         self._arr = (_lib.BatchItem * max(n, 1))()
@@ -213,8 +222,13 @@ class GemvBatch:
                                      "bfloat16 y")
             if packed.dtype != torch.uint8 or cb.dtype != torch.float32:
                 raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
-            if cb.shape != (N * K // 128, 8) or packed.numel() < packed_nbytes(N * K, 3):
-                raise ValueError(f"item {i}: not a 3-bit / 8-entry / block-128 {N}x{K} layer")
+            rows = (N + 3) // 4 * 4 if layout == "quad" else N
+            if cb.shape != (rows * K // 128, 8) or packed.numel() < packed_nbytes(rows * K, 3):
+                what = "row-quad layout of a" if layout == "quad" else "a"
+                raise ValueError(f"item {i}: not {what} 3-bit / 8-entry / block-128 {N}x{K} "
+                                 "layer")
+            if layout == "quad" and K < 2048:
+                raise ValueError(f"item {i}: the row-quad kernel needs K >= 2048 (got {K})")
             if yf != "silu_pairs" and (y.numel() != m * N or y.dtype not in _DT or
                                        not y.is_contiguous()):
                 shape = f"({m}, {N})" if m > 1 else f"({N},)"
@@ -239,12 +253,41 @@ class GemvBatch:
     def run(self):
         stream = ctypes.c_void_p(torch.cuda.current_stream(self.table.device).cuda_stream)
         lib = _lib.load()
-        if self.m == 1:
+        if self.layout == "quad":
+            _lib.check(lib.nb_gemm_skinny_quad_batched(self._arr, self.table.data_ptr(),
+                                                       self.count, self.m, _DT[self.y_dtype],
+                                                       stream))
+        elif self.m == 1:
             _lib.check(lib.nb_gemv_batched(self._arr, self.table.data_ptr(), self.count,
                                            _DT[self.y_dtype], stream))
         else:
             _lib.check(lib.nb_gemm_skinny_batched(self._arr, self.table.data_ptr(), self.count,
                                                   self.m, _DT[self.y_dtype], stream))
+
+
+def quad_layout(packed: torch.Tensor, codebook: torch.Tensor, N: int, K: int):
+    """The row-quad layout of a 3-bit / 8-entry / block-128 N x K layer
+    (nb_quad_layout): the same blocks, rows taken four at a time (N rounded
+    up with zero blocks), the four rows' blocks of one column block side by
+    side.  Returns (qpacked uint8, qcodebook (ceil(N/4)*4*K/128, 8) float32)
+    on the layer's device, for GemvBatch(..., layout="quad")."""
+    for name, t in (("packed", packed), ("codebook", codebook)):
+        _require_cuda(name, t)
+    _same_device(packed, codebook)
+    if packed.dtype != torch.uint8 or codebook.dtype != torch.float32:
+        raise TypeError("packed must be uint8 and codebook float32")
+    if K % 128 or codebook.shape != (N * K // 128, 8) or \
+            packed.numel() < packed_nbytes(N * K, 3):
+        raise ValueError(f"not a 3-bit / 8-entry / block-128 {N}x{K} layer")
+    if not packed.is_contiguous() or not codebook.is_contiguous():
+        raise ValueError("packed and codebook must be contiguous")
+    rows = (N + 3) // 4 * 4
+    lib = _lib.load()
+    qp = torch.empty(int(lib.nb_quad_layout_bytes(N, K)), dtype=torch.uint8, device=packed.device)
+    qc = torch.empty((rows * K // 128, 8), dtype=torch.float32, device=packed.device)
+    _lib.check(lib.nb_quad_layout(packed.data_ptr(), codebook.data_ptr(), N, K, qp.data_ptr(),
+                                  qc.data_ptr(), _stream(packed)))
+    return qp, qc
 
 
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
