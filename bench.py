@@ -92,6 +92,11 @@ def parse():
                    help="uniformly random index bytes and codebooks instead of quantized "
                         "N(0, 0.02) weights (same kernels and bytes; for profiled runs, where "
                         "the quantile/argmin generator's many small launches are slow)")
+    p.add_argument("--skinny-m", default="1,2,4,8,16",
+                   help="activation rows of the skinny configuration (comma list)")
+    p.add_argument("--no-per-matmul", action="store_true",
+                   help="skip the skinny configuration's one-launch-per-matmul comparison "
+                        "(182 launches a step; slow under counter collection)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="also time a plain 1 GiB device copy (the yardstick that scales "
                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
@@ -512,7 +517,7 @@ def bench_prefill(dev, random_weights=False):
     return out
 
 
-def bench_skinny(dev, layers):
+def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
     """Config 2: M activation rows over all 182 matmuls of a step.
 
     batched: one launch per step -- nb_gemv_batched (the streaming kernel)
@@ -527,7 +532,7 @@ def bench_skinny(dev, layers):
     quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats]
     torch.cuda.synchronize()
     out = {}
-    for M in (1, 2, 4, 8, 16):
+    for M in ms:
         xs = {K: synth.make_activation(K, m=M, seed=M, device=dev, dtype=torch.bfloat16)
               for K in (2560, 6912)}
         ys = [torch.empty(M, m.N, device=dev) for m in mats]
@@ -555,12 +560,12 @@ def bench_skinny(dev, layers):
         def run():
             for m, y in zip(mats, ys):
                 ops.gemv(xs[m.K], m.packed, m.cb, m.N, m.K, out=y)
-        ms_p = graph_time(run, 20, 5)
+        ms_p = graph_time(run, 20, 5) if per_matmul else float("nan")
         out[f"M{M}"] = {"us_per_step": round(ms_b * 1e3, 1), "GB_s": round(nbytes / ms_b / 1e6, 1),
                         "pct_hbm_peak": round(nbytes / ms_b / 1e6 / HBM_PEAK_GBS * 100, 1),
                         "TFLOP_s": round(fl / ms_b / 1e9, 2), "kernel": kernel, **extra,
-                        "per_matmul_us_per_step": round(ms_p * 1e3, 1),
-                        "per_matmul_GB_s": round(nbytes / ms_p / 1e6, 1)}
+                        "per_matmul_us_per_step": round(ms_p * 1e3, 1) if per_matmul else None,
+                        "per_matmul_GB_s": round(nbytes / ms_p / 1e6, 1) if per_matmul else None}
         log(f"[bench] skinny M={M}: batched {ms_b*1e3:.1f} us ({nbytes/ms_b/1e6:.0f} GB/s, "
             f"{kernel}), per-matmul launches {ms_p*1e3:.1f} us")
         del ys, xs, batch
@@ -847,7 +852,9 @@ def main():
         for name, fn in (("config0", lambda: bench_config0(dev, not args.no_cpu_baseline)),
                          ("decode", lambda: bench_decode(dev, args.decode_tokens)),
                          ("prefill", lambda: bench_prefill(dev, args.random_weights)),
-                         ("skinny", lambda: bench_skinny(dev, layers)),
+                         ("skinny", lambda: bench_skinny(
+                             dev, layers, tuple(int(v) for v in args.skinny_m.split(",")),
+                             not args.no_per_matmul)),
                          ("sweep", lambda: bench_sweep(dev)),
                          ("quantize", lambda: bench_quantize(dev)),
                          ("codec", lambda: bench_codec(dev))):

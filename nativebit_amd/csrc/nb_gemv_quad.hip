@@ -456,22 +456,31 @@ static int launch_quad_group(const StreamProblem* dev_probs, const StreamProblem
         return qbeg[p] + (int)((r + hp[p].bpr - 1) / hp[p].bpr);
     };
     // Workgroup runs balanced by pairs (each an equal share of what is left);
-    // a run whose x staging does not fit beside the 8-wave ring ends at the
-    // start of its last problem (one problem's always fits: checked above).
+    // a run whose x staging does not fit beside the ring ends at the start
+    // of its last problem (one problem's always fits the 8-wave ring:
+    // checked above).  The 12-wave ring is planned first; when its runs
+    // would need more workgroups than the device has CUs, the 8-wave one.
     const int G = std::max(1, std::min(device_cu_count(), total_q));
-    std::vector<int> wq{0};
-    while (wq.back() < total_q) {
-        const int q0 = wq.back();
-        const int64_t done = pairs_at(q0);
-        const int left = std::max(1, G - ((int)wq.size() - 1));
-        int q1 = std::max(q0 + 1, std::min(total_q, quad_at(done + (total_pairs - done) / left)));
-        while (ring8 + quad_x_bytes(hp, qbeg.data(), nprob, q0, q1, M) > lds_max) {
-            const int p = (int)(std::upper_bound(qbeg.begin(), qbeg.end(), q1 - 1) -
-                                qbeg.begin()) - 1;
-            q1 = qbeg[p];   // > q0: a run inside one problem fits
+    auto plan = [&](int64_t ring) {
+        std::vector<int> wq{0};
+        while (wq.back() < total_q) {
+            const int q0 = wq.back();
+            const int64_t done = pairs_at(q0);
+            const int left = std::max(1, G - ((int)wq.size() - 1));
+            int q1 = std::max(q0 + 1,
+                              std::min(total_q, quad_at(done + (total_pairs - done) / left)));
+            while (ring + quad_x_bytes(hp, qbeg.data(), nprob, q0, q1, M) > lds_max) {
+                const int p = (int)(std::upper_bound(qbeg.begin(), qbeg.end(), q1 - 1) -
+                                    qbeg.begin()) - 1;
+                if (qbeg[p] <= q0) return std::vector<int>();   // one problem does not fit
+                q1 = qbeg[p];
+            }
+            wq.push_back(q1);
         }
-        wq.push_back(q1);
-    }
+        return wq;
+    };
+    std::vector<int> wq = plan(ring12);
+    if (wq.empty() || (int)wq.size() - 1 > G) wq = plan(ring8);
     const int nruns = (int)wq.size() - 1;
     for (int r0 = 0; r0 < nruns; r0 += kStreamMaxGroups) {
         const int n = std::min(kStreamMaxGroups, nruns - r0);
