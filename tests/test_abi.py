@@ -264,6 +264,37 @@ def test_skinny_batch_validation():
     assert sk(empty, None, 1, 4, _lib.NB_F32, None) == _lib.NB_OK
 
 
+def test_quad_batch_and_layout_validation():
+    """nb_gemm_skinny_quad_batched: M <= 4, K >= 2048, plus the skinny
+    checks; nb_quad_layout: shape, pointers and alignment; the layout's
+    byte count (ceil(N / 4) * 4 rows of K / 128 blocks of 48 bytes)."""
+    lib = _lib.load()
+    Item = _lib.BatchItem
+    good = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 2048))
+    qs = lib.nb_gemm_skinny_quad_batched
+    for M in (0, 5, 16):
+        assert qs(good, FAKE, 1, M, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert _lib.last_error().startswith("nb_gemm_skinny_quad_batched")
+    short = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 1920))
+    assert qs(short, FAKE, 1, 4, _lib.NB_F32, None) == _lib.NB_EUNSUPPORTED
+    assert qs(good, None, 1, 4, _lib.NB_F32, None) == _lib.NB_EINVAL
+    add16 = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 2048, 0, _lib.NB_Y_ADD, None, 0.0, 0))
+    assert qs(add16, FAKE, 1, 2, _lib.NB_BF16, None) == _lib.NB_EUNSUPPORTED
+    empty = (Item * 1)(Item(None, None, None, None, 0, 2048))
+    assert qs(empty, None, 1, 4, _lib.NB_F32, None) == _lib.NB_OK
+    assert lib.nb_quad_layout_bytes(8, 2048) == 8 * 16 * 48
+    assert lib.nb_quad_layout_bytes(9, 256) == 12 * 2 * 48
+    assert lib.nb_quad_layout_bytes(0, 256) == 0 and lib.nb_quad_layout_bytes(4, 200) == 0
+    ql = lib.nb_quad_layout
+    assert ql(FAKE, FAKE, 8, 200, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert ql(FAKE, FAKE, 8, 8320, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert ql(FAKE, FAKE, -1, 256, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert ql(None, FAKE, 8, 256, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert ql(FAKE, FAKE, 8, 256, FAKE + 8, FAKE, None) == _lib.NB_EALIGN
+    assert _lib.last_error().startswith("nb_quad_layout")
+    assert ql(None, None, 0, 256, None, None, None) == _lib.NB_OK
+
+
 # --- prefill and decode-step entry points: host-side validation -------------
 
 def prefill(**kw):
