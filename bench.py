@@ -433,6 +433,29 @@ def event_time(fn, reps, warmup=3, settle_s=SETTLE_S):
     return s.elapsed_time(e) / reps
 
 
+def graph_calls_time(fn, calls=10, reps=10, settle_s=SETTLE_S):
+    """ms per call of fn() with `calls` calls captured back to back in one
+    HIP graph, replayed `reps` times (after settle_s seconds of untimed
+    replays): GPU time per call including the launch gaps inside a graph,
+    without the host's per-call Python and ctypes cost."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    if settle_s > 0:
+        _settle(g.replay, settle_s, cap=2000)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / (calls * reps)
+
+
 def bench_decode(dev, n_gen=256):
     """Config 4b: greedy decode tokens/s of a random-init 2.2B packed model
     (one HIP graph of launches replayed per token)."""
@@ -468,12 +491,14 @@ PREFILL_SHAPES = (("qkv", 7680, 2560), ("o", 2560, 2560), ("gate|up", 13824, 256
 def bench_prefill(dev, random_weights=False):
     """Config 4a: prefill-sized contraction with the packed weights.
 
-    The value is nb_gemm_prefill: the hand-written MFMA kernels that
-    dequantize the 3-bit stream into LDS tiles.  Beside it, for comparison
-    only: nb_gemm_prefill_ws (the weight expanded to bf16 in a workspace,
+    The value is nb_gemm_prefill_split (ops.gemm_prefill's default): the
+    hand-written MFMA kernels that dequantize the 3-bit stream into LDS
+    tiles, split over K ranges where one launch's tile grid would leave CUs
+    idle; beside it the one-launch kernel (nb_gemm_prefill) and, for
+    comparison only, nb_gemm_prefill_ws (the weight expanded to bf16 in a workspace,
     then hipBLASLt) and torch's dense bf16 matmul of an already-unpacked
     weight."""
-    from nativebit_amd import ops, synth
+    from nativebit_amd import _lib, ops, synth
     layers = {n: _make(random_weights)(N, K, seed=50 + i, device=dev)
               for i, (n, N, K) in enumerate(PREFILL_SHAPES)}
     out = {}
@@ -484,14 +509,24 @@ def bench_prefill(dev, random_weights=False):
         for n, N, K in PREFILL_SHAPES:
             lay = layers[n]
             y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-            ms = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y),
-                            20)
-            ms_blas = event_time(lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K,
-                                                          out=y, path="blas"), 20)
             w = torch.empty(N, K, dtype=torch.bfloat16, device=dev).normal_()
-            ms_ref = event_time(lambda: torch.matmul(xs[K], w.T), 20)
+            fns = [lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y),
+                   lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y,
+                                            path="fused"),
+                   lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y,
+                                            path="blas"),
+                   lambda: torch.matmul(xs[K], w.T)]
+            # each form timed twice, in alternation, and the lower time kept
+            # (the first graph timed after a shape change can run up to ~30 %
+            # slow while the clocks settle)
+            t = [min(a, b) for a, b in zip([graph_calls_time(f) for f in fns],
+                                           [graph_calls_time(f) for f in fns])]
+            ms, ms_one, ms_blas, ms_ref = t
             fl = 2 * M * N * K
+            ws = int(_lib.load().nb_gemm_prefill_split_ws_bytes(M, N, K))
             per[n] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / ms / 1e9, 1),
+                      "k_split_partials_MiB": round(ws / 2**20, 2),
+                      "one_launch_us": round(ms_one * 1e3, 1),
                       "blas_workspace_us": round(ms_blas * 1e3, 1),
                       "torch_dense_bf16_us": round(ms_ref * 1e3, 1)}
             tot_ms += ms
@@ -506,9 +541,14 @@ def bench_prefill(dev, random_weights=False):
                         "blas_workspace_layer_us": round(blas_ms * 1e3, 1),
                         "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
                         "per_matmul": per}
-    out["note"] = ("us / TFLOP_s: nb_gemm_prefill, the hand-written MFMA kernels that read the "
-                   "3-bit stream and codebooks and dequantize into LDS (bf16 operands, fp32 "
-                   "accumulation, bf16 y); comparison columns only: blas_workspace = "
+    out["note"] = ("us / TFLOP_s: nb_gemm_prefill_split, the hand-written MFMA kernels that "
+                   "read the 3-bit stream and codebooks and dequantize into LDS (bf16 operands, "
+                   "fp32 accumulation, bf16 y), with a K split (fp32 partials in a workspace, "
+                   "one reduction launch) where the tile grid would leave CUs idle "
+                   "(k_split_partials_MiB > 0); one_launch = nb_gemm_prefill (no split); "
+                   "every column is GPU time per call, 10 calls per HIP graph replay, the "
+                   "lower of two timings; "
+                   "comparison columns only: blas_workspace = "
                    "nb_gemm_prefill_ws (W expanded to bf16 in a workspace by the format kernel, "
                    "then one hipBLASLt GEMM, the expansion inside the timed call), "
                    "torch_dense_bf16 = torch.matmul on an already-unpacked bf16 weight (the "

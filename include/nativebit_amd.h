@@ -109,6 +109,28 @@ int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed, const flo
                     void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* stream);
 
 /*
+ * nb_gemm_prefill with a caller workspace for a K split: where the tile
+ * grid of one launch would leave CUs idle (few tokens or a narrow layer:
+ * every workgroup would walk all of K with little work per step), the
+ * kernel runs over up to 8 K ranges per tile and writes fp32 partial
+ * products [S][M][N] to the workspace, and a second launch adds them in
+ * range order and writes y.  The workspace needs
+ * nb_gemm_prefill_split_ws_bytes(M, N, K) bytes (0 where the shape is not
+ * split; then `workspace` may be NULL), 256-byte aligned, contents
+ * clobbered; a smaller ws_bytes is NB_EINVAL.  Same operands and result
+ * contract as nb_gemm_prefill; results are deterministic and differ from
+ * nb_gemm_prefill's only by fp32 summation order where a split is used.
+ * Replaces: the same batched branch of PackedLinear.forward in its bf16
+ *           form (inference/triton_kernel.py:258-275, inference/eval_ppl.py:
+ *           149-174); the workspace follows the caller-allocates convention
+ *           of the rest of this interface.
+ */
+int64_t nb_gemm_prefill_split_ws_bytes(int M, int N, int K);
+int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* packed,
+                          const float* codebook, void* y, int y_dtype, int64_t ldy, int M, int N,
+                          int K, void* workspace, int64_t ws_bytes, void* stream);
+
+/*
  * nb_gemm_prefill with a caller workspace (>= nb_gemm_prefill_ws_bytes(M, N,
  * K) bytes, 256-byte aligned, contents clobbered): W is expanded to bf16 in
  * the workspace by the format kernel and y = x . W^T is one hipBLASLt GEMM

@@ -738,15 +738,21 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
 
 }  // extern "C"
 
-extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed,
-                               const float* codebook, void* y, int y_dtype, int64_t ldy, int M,
-                               int N, int K, void* stream) {
-    const char* fn = "nb_gemm_prefill";
+namespace {
+// Argument checks shared by the fused prefill entry points; NB_OK (then
+// M, N > 0) or a status, with *done set for an empty product.
+int check_prefill(const char* fn, const void* x, int64_t ldx, const uint8_t* packed,
+                  const float* codebook, const void* y, int y_dtype, int64_t ldy, int M, int N,
+                  int K, bool* done) {
+    *done = false;
     if (M < 0 || N < 0 || K < 0) return fail(NB_EINVAL, "%s: negative shape", fn);
     if (K % 128 != 0) return fail(NB_EUNSUPPORTED, "%s: K=%d not a multiple of 128", fn, K);
     if ((int64_t)N * (K / 128) >= (1LL << 31)) return fail(NB_EUNSUPPORTED, "%s: too many blocks", fn);
     if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
-    if (M == 0 || N == 0) return NB_OK;
+    if (M == 0 || N == 0) {
+        *done = true;
+        return NB_OK;
+    }
     if (K == 0) return fail(NB_EUNSUPPORTED, "%s: K == 0 (use nb_gemv)", fn);
     if (ldx < K || ldy < N) return fail(NB_EINVAL, "%s: ldx=%lld < K or ldy=%lld < N", fn,
                                         (long long)ldx, (long long)ldy);
@@ -754,9 +760,50 @@ extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed
     if (!aligned(x, 16) || ldx % 8 != 0) return fail(NB_EALIGN, "%s: x must be 16-byte aligned with ldx %% 8 == 0", fn);
     if (!aligned(packed, 8) || !aligned(codebook, 16)) return fail(NB_EALIGN, "%s: packed 8- / codebook 16-byte alignment", fn);
     if (!aligned(y, dtype_size(y_dtype))) return fail(NB_EALIGN, "%s: y not aligned to its dtype", fn);
-    int st = ensure_device();
+    return NB_OK;
+}
+}  // namespace
+
+extern "C" int nb_gemm_prefill(const void* x, int64_t ldx, const uint8_t* packed,
+                               const float* codebook, void* y, int y_dtype, int64_t ldy, int M,
+                               int N, int K, void* stream) {
+    bool done;
+    int st = check_prefill("nb_gemm_prefill", x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
+                           &done);
+    if (st || done) return st;
+    st = ensure_device();
     if (st) return st;
+    return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K, nullptr, 0,
+                           static_cast<hipStream_t>(stream));
+}
+
+extern "C" int64_t nb_gemm_prefill_split_ws_bytes(int M, int N, int K) {
+    // without a usable device the plan assumes 256 CUs (and no error is left)
+    if (ensure_device() != NB_OK) g_last_error[0] = '\0';
+    return prefill_split_bytes(M, N, K);
+}
+
+extern "C" int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* packed,
+                                     const float* codebook, void* y, int y_dtype, int64_t ldy,
+                                     int M, int N, int K, void* workspace, int64_t ws_bytes,
+                                     void* stream) {
+    const char* fn = "nb_gemm_prefill_split";
+    bool done;
+    int st = check_prefill(fn, x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K, &done);
+    if (st || done) return st;
+    if (ws_bytes < 0) return fail(NB_EINVAL, "%s: ws_bytes=%lld", fn, (long long)ws_bytes);
+    if (!aligned(workspace, 256)) return fail(NB_EALIGN, "%s: workspace not 256-byte aligned", fn);
+    // the size check comes before the device's status, so that it holds (for
+    // 256 CUs) where there is no device
+    const int dev_st = ensure_device();
+    const int64_t need = prefill_split_bytes(M, N, K);
+    if (ws_bytes < need || (need > 0 && !workspace)) {
+        return fail(NB_EINVAL, "%s: workspace of %lld bytes < %lld", fn, (long long)ws_bytes,
+                    (long long)need);
+    }
+    if (dev_st) return dev_st;
     return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
+                           need > 0 ? workspace : nullptr, ws_bytes,
                            static_cast<hipStream_t>(stream));
 }
 

@@ -127,9 +127,15 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
 
 
 // Prefill GEMM with a packed weight (nb_prefill2.hip): the packed weight
-// dequantized into LDS tiles, bf16 MFMAs; arguments validated.
+// dequantized into LDS tiles, bf16 MFMAs; arguments validated.  With a
+// workspace of at least prefill_split_bytes(M, N, K) bytes, a layer whose
+// tile grid leaves CUs idle is split over K ranges (fp32 partial products in
+// the workspace, then one reduction launch); otherwise (workspace null) one
+// launch over all of K.
 int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
-                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream);
+                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
+                    int64_t ws_bytes, hipStream_t stream);
+int64_t prefill_split_bytes(int M, int N, int K);
 
 // hipBLASLt's own share of the prefill workspace, after the bf16 weight.
 constexpr int64_t kPrefillBlasWorkspace = 32ll << 20;

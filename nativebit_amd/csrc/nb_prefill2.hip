@@ -105,6 +105,8 @@ struct Prefill2Args {
     int64_t ldy;
     int y_dtype;
     int M, N, K;
+    int ksplit;   // K ranges per output tile (1: the whole of K)
+    float* part;  // ksplit > 1: fp32 partial products [ksplit][M][N], else null
 };
 
 // One thread's share of a W slice: 12 index bytes (32 weights) per half
@@ -142,15 +144,23 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     // contiguous run of the tiles in (token tile, output tile) order, so
     // its workgroups share one or two token tiles of X in its L2 rather
     // than all of them.
+    // With a K split, virtual tile v is K range v / ntiles of output tile
+    // v % ntiles, so an XCD's run holds neighbouring tiles of one K range
+    // (which share their X slices).
     const int nn = (a.N + BN - 1) / BN;
-    int tile;
+    const int ntiles = nn * ((a.M + BM - 1) / BM);
+    int tile, ks;
     {
         const int T = gridDim.x, g = blockIdx.x, full = T / 8, rem = T % 8, x = g % 8;
-        tile = x * full + min(x, rem) + g / 8;
+        const int v = x * full + min(x, rem) + g / 8;
+        ks = v / ntiles;
+        tile = v - ks * ntiles;
     }
     const int n0 = (tile % nn) * BN, m0 = (tile / nn) * BM;
     const int bpr = a.K / 128;
-    const int nsteps = a.K / kBK;
+    // this workgroup's K steps: [s0, s0 + nsteps) of the K / 64
+    const int s0 = (int)((int64_t)ks * (a.K / kBK) / a.ksplit);
+    const int nsteps = (int)((int64_t)(ks + 1) * (a.K / kBK) / a.ksplit) - s0;
     const uint32_t base = lds_addr(smem);
 
     // X slice: instruction i of wave w covers slice rows 8 (kXLoads w + i)
@@ -162,7 +172,7 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
             const int r = r0 + (lane >> 3);
             const int c = (lane & 7) ^ (r & 7);
             const int gm = min(m0 + r, a.M - 1);
-            const uint16_t* src = a.x + (int64_t)gm * a.ldx + (int64_t)step * kBK + c * 8;
+            const uint16_t* src = a.x + (int64_t)gm * a.ldx + (int64_t)(s0 + step) * kBK + c * 8;
             dma16(__builtin_amdgcn_readfirstlane(base + stage * kStage + r0 * kRowBytes), src);
         }
     };
@@ -172,11 +182,11 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     const bool deq = kAllDeq || tid < 2 * BN;
     auto load_w = [&](int step, WR& w) {
         if (!deq) return;
-        const int64_t blk = (int64_t)gn * bpr + (step >> 1);
+        const int64_t blk = (int64_t)gn * bpr + ((s0 + step) >> 1);
 #pragma unroll
         for (int h = 0; h < H; ++h) {
             const uint32_t* ip = reinterpret_cast<const uint32_t*>(
-                a.packed + blk * 48 + (step & 1) * 24 + (h0 + h) * 12);
+                a.packed + blk * 48 + ((s0 + step) & 1) * 24 + (h0 + h) * 12);
             w.d[h].x = ip[0];
             w.d[h].y = ip[1];
             w.d[h].z = ip[2];
@@ -277,7 +287,13 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     }
 
     // D fragment (i, j): lane holds outputs n = 4 fq .. 4 fq + 3 of A sub-tile
-    // i for token fr of B sub-tile j
+    // i for token fr of B sub-tile j.  With a K split, the fp32 partial
+    // products go to plane ks of `part` (row stride N), summed by
+    // prefill_reduce_kernel.
+    const bool partial = a.part != nullptr;
+    const int y_dtype = partial ? NB_F32 : a.y_dtype;
+    void* const yb = partial ? static_cast<void*>(a.part + (int64_t)ks * a.M * a.N) : a.y;
+    const int64_t ldy = partial ? a.N : a.ldy;
 #pragma unroll
     for (int i = 0; i < TI; ++i) {
         const int n = n0 + wn * WN + i * 16 + fq * 4;
@@ -286,9 +302,9 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
             const int m = m0 + wm * WM + j * 16 + fr;
             if (m >= a.M) continue;
             const f32x4_t v = acc[i][j];
-            if (a.y_dtype == NB_BF16) {
-                bf16_bits* yp = static_cast<bf16_bits*>(a.y) + (int64_t)m * a.ldy + n;
-                if (n + 3 < a.N && ((a.ldy | n) & 3) == 0) {
+            if (y_dtype == NB_BF16) {
+                bf16_bits* yp = static_cast<bf16_bits*>(yb) + (int64_t)m * ldy + n;
+                if (n + 3 < a.N && ((ldy | n) & 3) == 0) {
                     u32x2_t p;
                     p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
                     p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
@@ -299,8 +315,8 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
                         if (n + e < a.N) yp[e] = f32_to_bf16_rne(v[e]);
                 }
             } else {
-                float* yp = static_cast<float*>(a.y) + (int64_t)m * a.ldy + n;
-                if (n + 3 < a.N && ((a.ldy | n) & 3) == 0) {
+                float* yp = static_cast<float*>(yb) + (int64_t)m * ldy + n;
+                if (n + 3 < a.N && ((ldy | n) & 3) == 0) {
                     *reinterpret_cast<f32x4_t*>(yp) = v;
                 } else {
 #pragma unroll
@@ -312,10 +328,97 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     }
 }
 
+// y[m][n] = sum over k ranges s = 0, 1, ... of part[s][m][n] (in that
+// order, so the result does not depend on which workgroup finished first),
+// converted to y's dtype.  Four consecutive outputs per thread where the
+// rows allow it.
+__global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __restrict__ part,
+                                                             int S, int M, int N, void* y,
+                                                             int y_dtype, int64_t ldy) {
+    const int64_t plane = (int64_t)M * N;
+    const bool vec = ((N | ldy) & 3) == 0;
+    const int64_t total = vec ? plane / 4 : plane;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        if (vec) {
+            const int64_t e = 4 * i, m = e / N, n = e - m * N;
+            f32x4_t v = *reinterpret_cast<const f32x4_t*>(part + e);
+            for (int k = 1; k < S; ++k) v += *reinterpret_cast<const f32x4_t*>(part + k * plane + e);
+            if (y_dtype == NB_BF16) {
+                u32x2_t p;
+                p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+                p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+                *reinterpret_cast<u32x2_t*>(static_cast<bf16_bits*>(y) + m * ldy + n) = p;
+            } else {
+                *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + m * ldy + n) = v;
+            }
+        } else {
+            const int64_t m = i / N, n = i - m * N;
+            float v = part[i];
+            for (int k = 1; k < S; ++k) v += part[k * plane + i];
+            if (y_dtype == NB_BF16) {
+                static_cast<bf16_bits*>(y)[m * ldy + n] = f32_to_bf16_rne(v);
+            } else {
+                static_cast<float*>(y)[m * ldy + n] = v;
+            }
+        }
+    }
+}
+
+struct PrefillPlan {
+    int BM, BN, S;
+};
+
+// The tile (BM tokens x BN outputs) and the number of K ranges per tile.
+// One launch over all of K: the largest tile (fewest workgroups, least
+// redundant traffic) whose grid still gives about 0.6 workgroups per CU.
+// Where only the smallest tile (64 x 128) is left -- few tokens or a narrow
+// layer, where every workgroup walks all of K with little work per step --
+// and a split is allowed, the largest tile that reaches that grid when
+// repeated over S <= 8 K ranges of at least 8 steps each, preferring fp32
+// partial products (written, then read once by the reduction) of at most
+// twice the packed weight's bytes, else four times.  Measured on MI355X
+// over the four 2.2B layer shapes: M = 128 layer 140 -> 86 us, M = 512
+// 191 -> 156 us (down 75 -> 44, o 28 -> 24), M = 2048 unchanged (no split);
+// splitting tiles that already fill the grid was slower.
+PrefillPlan prefill_plan(int M, int N, int K, bool allow_split) {
+    const int64_t cus = device_cu_count();
+    const int64_t want = cus * 3 / 5;
+    const int nsteps = K / kBK;
+    const int64_t wbytes = (int64_t)N * K / 128 * 80;
+    auto groups = [&](int bm, int bn) {
+        return (int64_t)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
+    };
+    const int tiles[4][2] = {{256, 256}, {256, 128}, {128, 128}, {64, 128}};
+    for (int t = 0; t < 3; ++t) {
+        if (groups(tiles[t][0], tiles[t][1]) >= want) return {tiles[t][0], tiles[t][1], 1};
+    }
+    if (allow_split) {
+        for (int64_t mult = 2; mult <= 4; mult += 2) {
+            for (int t = 0; t < 4; ++t) {
+                const int bm = tiles[t][0], bn = tiles[t][1];
+                if (bm > std::max(64, M)) continue;   // mostly empty token rows
+                const int64_t g = groups(bm, bn);
+                int S = (int)std::min<int64_t>({cus / g, 8, nsteps / 8});
+                while (S > 1 && (int64_t)S * M * N * 4 > mult * wbytes) --S;
+                if (S > 1 && g * S >= want) return {bm, bn, S};
+            }
+        }
+    }
+    return {64, 128, 1};
+}
+
 }  // namespace
 
+int64_t prefill_split_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+    const PrefillPlan p = prefill_plan(M, N, K, true);
+    return p.S > 1 ? (int64_t)p.S * M * N * 4 : 0;
+}
+
 int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
-                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, hipStream_t stream) {
+                    void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
+                    int64_t ws_bytes, hipStream_t stream) {
     Prefill2Args a;
     a.x = static_cast<const uint16_t*>(x);
     a.ldx = ldx;
@@ -327,31 +430,33 @@ int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const flo
     a.M = M;
     a.N = N;
     a.K = K;
+    PrefillPlan p = prefill_plan(M, N, K, workspace != nullptr);
+    if (p.S > 1 && ws_bytes < (int64_t)p.S * M * N * 4) p = prefill_plan(M, N, K, false);
+    a.ksplit = p.S;
+    a.part = p.S > 1 ? static_cast<float*>(workspace) : nullptr;
     constexpr int W = NB_PREFILL_WAVES;
-    // The largest tile (fewest workgroups, least redundant traffic) whose
-    // grid still gives about 0.6 workgroups per CU; where none does (few
-    // tokens, narrow layers), the smallest, for the most workgroups.
-    // (Measured on MI355X over the four 2.2B layer shapes at M = 128, 512
-    // and 2048: this choice was the fastest tile, or within 1 % of it, in
-    // all twelve cases.)
-    const int64_t want = (int64_t)device_cu_count() * 3 / 5;
-    auto groups = [&](int bm, int bn) {
-        return (int64_t)((N + bn - 1) / bn) * ((M + bm - 1) / bm);
-    };
+    const unsigned grid = (unsigned)(((N + p.BN - 1) / p.BN) * ((M + p.BM - 1) / p.BM) * p.S);
 #define NB_PREFILL2_LAUNCH(BMv, BNv)                                                          \
-    hipLaunchKernelGGL((prefill2_kernel<BMv, BNv, W>),                                      \
-                       dim3((unsigned)groups(BMv, BNv)), dim3(64 * W),                       \
+    hipLaunchKernelGGL((prefill2_kernel<BMv, BNv, W>), dim3(grid), dim3(64 * W),             \
                        (size_t)2 * (BMv + BNv) * kRowBytes, stream, a)
-    if (groups(256, 256) >= want) {
+    if (p.BM == 256 && p.BN == 256) {
         NB_PREFILL2_LAUNCH(256, 256);
-    } else if (groups(256, 128) >= want) {
+    } else if (p.BM == 256) {
         NB_PREFILL2_LAUNCH(256, 128);
-    } else if (groups(128, 128) >= want) {
+    } else if (p.BM == 128) {
         NB_PREFILL2_LAUNCH(128, 128);
     } else {
         NB_PREFILL2_LAUNCH(64, 128);
     }
 #undef NB_PREFILL2_LAUNCH
+    if (p.S > 1) {
+        const int st = check_launch("nb_gemm_prefill");
+        if (st) return st;
+        const int64_t items = ((N | ldy) & 3) == 0 ? (int64_t)M * N / 4 : (int64_t)M * N;
+        const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 4096);
+        hipLaunchKernelGGL(prefill_reduce_kernel, dim3(rg), dim3(256), 0, stream, a.part, p.S,
+                           M, N, y, y_dtype, ldy);
+    }
     return check_launch("nb_gemm_prefill");
 }
 

@@ -122,7 +122,8 @@ int launch_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed, const f
     if (!plan.ok) {
         // no library algorithm for this shape: the fused kernel computes it
         if (!cached) destroy(local);
-        return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K, stream);
+        return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K, nullptr, 0,
+                               stream);
     }
     const int64_t total = (int64_t)N * K;
     int st = launch_dequant(packed, codebook, w, NB_BF16, total, total / 128, 3, 8, 128, stream);

@@ -267,7 +267,9 @@ class DecodeEngine(_DecoderBase):
         """Feed the whole prompt as one batched pass -- the reference's
         prompt forward over T tokens (generate_torch.py:299-302) -- and choose
         the first generated token: per layer the q|k|v, o, gate|up and down
-        matmuls are packed MFMA contractions over the T rows (nb_gemm_prefill),
+        matmuls are packed MFMA contractions over the T rows
+        (nb_gemm_prefill_split: at T = 128 each layer's tile grid is small,
+        so the kernel runs over K ranges with fp32 partials in a workspace),
         RoPE and the cache appends are nb_rope_kv_rows, causal attention is
         nb_attention_rows, and the norms with their residual adds are
         nb_rmsnorm_rows; the last row's final norm feeds nb_lm_head_argmax.

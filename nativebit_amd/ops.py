@@ -296,8 +296,12 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
     """y = x @ bf16(W).T for a 3-bit / 8-entry / block-128 packed W (N x K);
     x (M, K) bfloat16, row-contiguous, fp32 accumulation.
 
-    ``path``: "fused" or "auto" (nb_gemm_prefill: the packed weight is
-    dequantized into LDS inside the hand-written MFMA kernels), or "blas"
+    ``path``: "auto" (nb_gemm_prefill_split: the hand-written MFMA kernel,
+    the packed weight dequantized into LDS tiles; a layer whose tile grid
+    would leave CUs idle -- few tokens, narrow layers -- is split over K
+    ranges, with fp32 partial products in a workspace taken from torch's
+    allocator and one reduction launch), "fused" (nb_gemm_prefill: the same
+    kernel in one launch over all of K, no workspace), or "blas"
     (nb_gemm_prefill_ws: W expanded to bf16 in a workspace, then one
     hipBLASLt GEMM -- kept as a comparison)."""
     for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
@@ -325,6 +329,14 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
         _lib.check(lib.nb_gemm_prefill_ws(
             x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
             _DT[out.dtype], out.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x)))
+        return out
+    if path == "auto":
+        nbytes = int(lib.nb_gemm_prefill_split_ws_bytes(M, N, K))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
+        _lib.check(lib.nb_gemm_prefill_split(
+            x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
+            _DT[out.dtype], out.stride(0), M, N, K, ws.data_ptr() if nbytes else None, nbytes,
+            _stream(x)))
         return out
     _lib.check(lib.nb_gemm_prefill(
         x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),

@@ -361,6 +361,51 @@ def test_prefill_ws_empty_is_ok():
     assert prefill_ws(M=0) == _lib.NB_OK and prefill_ws(N=0) == _lib.NB_OK
 
 
+def prefill_split(**kw):
+    lib = _lib.load()
+    a = dict(x=FAKE, ldx=2560, packed=FAKE, codebook=FAKE, y=FAKE, y_dtype=_lib.NB_BF16,
+             ldy=2560, M=128, N=2560, K=2560, ws=FAKE,
+             ws_bytes=int(lib.nb_gemm_prefill_split_ws_bytes(128, 2560, 2560)), stream=None)
+    a.update(kw)
+    return lib.nb_gemm_prefill_split(*a.values())
+
+
+def test_prefill_split_ws_bytes():
+    """K ranges (fp32 partial products M x N each) only where the tile grid
+    would leave CUs idle: few tokens, narrow layers; none at M = 2048."""
+    lib = _lib.load()
+    b = lib.nb_gemm_prefill_split_ws_bytes
+    for N, K in ((7680, 2560), (2560, 2560), (13824, 2560), (2560, 6912)):
+        assert b(2048, N, K) == 0 and b(1024, N, K) == 0
+        s = b(128, N, K)
+        assert s > 0 and s % (128 * N * 4) == 0 and 2 <= s // (128 * N * 4) <= 8
+        # partial products at most four times the packed weight's bytes
+        assert s <= 4 * N * K // 128 * 80
+    assert b(512, 7680, 2560) == 0 and b(512, 2560, 6912) > 0
+    assert b(0, 64, 256) == 0 and b(32, 64, 200) == 0 and b(-1, 64, 256) == 0
+    assert b(128, 8, 128) == 0          # one step of K: nothing to split
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=200), _lib.NB_EUNSUPPORTED),
+    (dict(M=-1), _lib.NB_EINVAL),
+    (dict(ldy=100), _lib.NB_EINVAL),
+    (dict(y_dtype=7), _lib.NB_EINVAL),
+    (dict(ws=None), _lib.NB_EINVAL),
+    (dict(ws=FAKE + 16), _lib.NB_EALIGN),
+    (dict(ws_bytes=4096), _lib.NB_EINVAL),
+    (dict(ws_bytes=-1), _lib.NB_EINVAL),
+    (dict(x=FAKE + 8), _lib.NB_EALIGN),
+])
+def test_prefill_split_validation(kw, status):
+    assert prefill_split(**kw) == status
+    assert _lib.last_error().startswith("nb_gemm_prefill_split")
+
+
+def test_prefill_split_empty_is_ok():
+    assert prefill_split(M=0) == _lib.NB_OK and prefill_split(N=0) == _lib.NB_OK
+
+
 @pytest.mark.parametrize("kw,status", [
     (dict(n=0), _lib.NB_EINVAL),
     (dict(h_dtype=5), _lib.NB_EINVAL),

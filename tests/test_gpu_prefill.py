@@ -38,7 +38,7 @@ def layer(N, K, seed):
                                    (17, 2560, 2560), (512, 2560, 2560), (300, 7680, 2560),
                                    (64, 2560, 6912)])
 @pytest.mark.parametrize("ydt", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("path", ["fused", "blas"])
+@pytest.mark.parametrize("path", ["auto", "fused", "blas"])
 def test_prefill_vs_f64(dev, M, N, K, ydt, path):
     note(f"prefill M={M} N={N} K={K} {ydt} {path}")
     idx, p, cb = layer(N, K, M * 7 + N)
@@ -66,6 +66,64 @@ def test_prefill_strided_x_and_out(dev, path):
     w = torch.from_numpy(O.dequant(idx, cb, 128, N * K).reshape(N, K)).to(torch.bfloat16).float()
     ref = x.float().cpu() @ w.T
     assert rel(out.cpu(), ref) <= 1e-5
+
+
+# Shapes the K split takes (nb_gemm_prefill_split, path "auto"): few tokens
+# on every 2.2B layer shape, the 512-token narrow layers, and a ragged
+# shape whose N is not a multiple of 4 (scalar partial stores and sums).
+SPLIT_CASES = [(128, 7680, 2560), (128, 2560, 2560), (128, 13824, 2560), (128, 2560, 6912),
+               (512, 2560, 2560), (512, 2560, 6912), (100, 1998, 6912), (40, 2560, 6912)]
+
+
+@pytest.mark.parametrize("M,N,K", SPLIT_CASES)
+def test_prefill_split_vs_f64(dev, M, N, K):
+    """The split path against the fp64 brute force, deterministic over two
+    calls, and equal to the one-launch kernel up to fp32 summation order."""
+    from nativebit_amd import _lib
+    ws = _lib.load().nb_gemm_prefill_split_ws_bytes(M, N, K)
+    note(f"prefill split M={M} N={N} K={K} ws={ws}")
+    assert ws > 0
+    idx, p, cb = layer(N, K, 31 * M + N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)).to(torch.bfloat16)
+    xd, pd, cd = x.to(dev), torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    a = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=torch.float32, path="auto")
+    b = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=torch.float32, path="auto")
+    assert torch.equal(a, b)
+    one = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=torch.float32, path="fused")
+    assert rel(a.cpu(), one.cpu()) <= 1e-5, rel(a.cpu(), one.cpu())
+    y16 = ops.gemm_prefill(xd, pd, cd, N, K, out_dtype=torch.bfloat16, path="auto")
+    assert torch.equal(y16, a.to(torch.bfloat16))   # the sum, rounded once
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+    w = torch.from_numpy(w).to(torch.bfloat16).float().numpy()
+    rows = np.unique(np.linspace(0, M - 1, 16).astype(int))
+    ref = O.matmul_f64(x.float().numpy()[rows], w)
+    assert rel(a.cpu().numpy()[rows], ref) <= 1e-3, rel(a.cpu().numpy()[rows], ref)
+
+
+def test_prefill_split_strided_out_and_graph(dev):
+    """A split into a strided output (row stride N + 8) inside a HIP graph:
+    the workspace comes from the graph's pool, and every replay (eager work
+    in between) reproduces the eager result."""
+    M, N, K = 128, 2560, 2560
+    idx, p, cb = layer(N, K, 77)
+    x = torch.randn(M, K).to(torch.bfloat16).to(dev)
+    pd, cd = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    note("prefill split strided out + graph")
+    out = torch.full((M, N + 8), float("nan"), device=dev)[:, :N]
+    ops.gemm_prefill(x, pd, cd, N, K, out=out, path="auto")
+    torch.cuda.synchronize()
+    eager = out.clone()
+    w = torch.from_numpy(O.dequant(idx, cb, 128, N * K).reshape(N, K)).to(torch.bfloat16).float()
+    assert rel(eager.cpu(), x.float().cpu() @ w.T) <= 1e-5
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ops.gemm_prefill(x, pd, cd, N, K, out=out, path="auto")
+    for _ in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
 
 
 def test_prefill_matches_batched_gemv(dev):
