@@ -37,6 +37,7 @@ __device__ __forceinline__ float wsum(float v) { return wave64_sum(v); }
 // rmsnorm of T rows, one workgroup per row
 // ---------------------------------------------------------------------------
 constexpr int kNormThreads = 256;
+constexpr int kNormRegs = 16;      // elements per thread kept in registers (C <= 4096)
 
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows_kernel(
     float* __restrict__ x, const float* __restrict__ add, const float* __restrict__ emb,
@@ -47,7 +48,41 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows_kernel(
     float* xr = x + (int64_t)t * C;
     const float* src = tokens ? emb + (int64_t)tokens[t] * C : nullptr;
     const float* ar = add ? add + (int64_t)t * C : nullptr;
+    // rows of up to kNormRegs * 256 elements stay in registers between the
+    // sum of squares and the scaling, with every load issued up front
     float ss = 0.f;
+    if (C <= kNormRegs * kNormThreads) {
+        float v[kNormRegs], wv[kNormRegs];
+#pragma unroll
+        for (int j = 0; j < kNormRegs; ++j) {
+            const int i = threadIdx.x + j * kNormThreads;
+            const int ic = i < C ? i : 0;
+            v[j] = src ? src[ic] : xr[ic];
+            if (ar) v[j] = v[j] + ar[ic];
+            wv[j] = w[ic];
+        }
+#pragma unroll
+        for (int j = 0; j < kNormRegs; ++j) {
+            const int i = threadIdx.x + j * kNormThreads;
+            if (i < C) {
+                if (src || ar) xr[i] = v[j];
+                ss += v[j] * v[j];
+            }
+        }
+        ss = wsum(ss);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        float tot = 0.f;
+        for (int k = 0; k < kNormThreads / 64; ++k) tot += red[k];  // same order everywhere
+        const float norm = sqrtf(tot / (float)C + eps);
+#pragma unroll
+        for (int j = 0; j < kNormRegs; ++j) {
+            const int i = threadIdx.x + j * kNormThreads;
+            // (x / norm) * w, as generate_torch.py:37
+            if (i < C) store_out(h, h_dtype, (int64_t)t * C + i, (v[j] / norm) * wv[j]);
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < C; i += kNormThreads) {
         float v = src ? src[i] : xr[i];
         if (ar) v = v + ar[i];
@@ -112,37 +147,41 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ qkv, float* __rest
 // causal attention of T queries: grid (n_head, ceil(T / kQB)), 256 threads.
 // The workgroup holds kQB queries of one head and walks the keys in tiles
 // of kKT positions through LDS with an online softmax (running max and sum
-// per query); query t sees positions 0 .. pos0 + t.
+// per query); query t sees positions 0 .. pos0 + t.  Head dims past D (up
+// to a multiple of 4) are zero in LDS, so the dot products run over float4
+// pieces and add exact zeros.
 // ---------------------------------------------------------------------------
 constexpr int kQB = 16;       // queries per workgroup
 constexpr int kKT = 64;       // keys per tile
 constexpr int kAttThreads = 256;
 constexpr int kRowsMaxD = 128;
+constexpr int kQPitch = kRowsMaxD + 4;   // floats per LDS row of q and v (16-byte rows)
+constexpr int kKPitch = kKT + 4;         // floats per LDS row of k (one head dim)
 
 __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
     const float* __restrict__ q, const float* __restrict__ k_cache,
     const float* __restrict__ v_cache, int pos0, int T, void* __restrict__ out, int out_dtype,
     int n_head, int D, int ctx) {
-    __shared__ float qs[kQB][kRowsMaxD + 1];
-    __shared__ float ks[kRowsMaxD][kKT + 1];
-    __shared__ float vs[kKT][kRowsMaxD + 1];
-    __shared__ float ps[kQB][kKT + 1];
+    typedef __attribute__((ext_vector_type(4))) float f4;
+    __shared__ __align__(16) float qs[kQB][kQPitch];
+    __shared__ __align__(16) float ks[kRowsMaxD][kKPitch];   // keys transposed: [dim][position]
+    __shared__ __align__(16) float vs[kKT][kQPitch];
+    __shared__ __align__(16) float ps[kQB][kKPitch];
     const int hd = blockIdx.x, t0 = blockIdx.y * kQB;
     const int tid = threadIdx.x;
     const int C = n_head * D;
+    const int D4 = (D + 3) & ~3;
     const int nq = min(kQB, T - t0);
-    for (int e = tid; e < kQB * D; e += kAttThreads) {
-        const int i = e / D, d = e - i * D;
-        qs[i][d] = i < nq ? q[(int64_t)(t0 + i) * C + hd * D + d] : 0.f;
+    for (int e = tid; e < kQB * kQPitch; e += kAttThreads) {
+        const int i = e / kQPitch, d = e - i * kQPitch;
+        qs[i][d] = i < nq && d < D ? q[(int64_t)(t0 + i) * C + hd * D + d] : 0.f;
     }
-    // scores: thread (sq, sp) takes query sq and keys sp, sp + 16, sp + 32, sp + 48
+    // scores: thread (sq, sp) takes query sq and keys 4 sp .. 4 sp + 3
     const int sq = tid >> 4, sp = tid & 15;
-    // weighted values: thread (oq, og) takes query oq and dims og, og + 16, ...
+    // weighted values: thread (oq, og) takes query oq and dims 4 og .. 4 og + 3
+    // and 64 + 4 og .. 64 + 4 og + 3
     const int oq = tid >> 4, og = tid & 15;
-    constexpr int kDPer = kRowsMaxD / 16;
-    float o[kDPer];
-#pragma unroll
-    for (int j = 0; j < kDPer; ++j) o[j] = 0.f;
+    f4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;  // per query, kept by its 16 threads alike
     const int last = pos0 + t0 + nq - 1;  // the last position any query sees
     const float* kt = k_cache + (int64_t)hd * D * ctx;
@@ -150,25 +189,43 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
     for (int p0 = 0; p0 <= last; p0 += kKT) {
         const int np = min(kKT, last + 1 - p0);
         __syncthreads();  // the previous tile is no longer read
-        for (int e = tid; e < D * kKT; e += kAttThreads) {
-            const int d = e / kKT, p = e - d * kKT;
-            ks[d][p] = p < np ? kt[(int64_t)d * ctx + p0 + p] : 0.f;
+        // the tile's keys and values, all loads of a thread issued together
+        float kv[kRowsMaxD * kKT / kAttThreads], vv[kRowsMaxD * kKT / kAttThreads];
+#pragma unroll
+        for (int j = 0; j < kRowsMaxD * kKT / kAttThreads; ++j) {
+            const int e = tid + j * kAttThreads;
+            const int d = e / kKT, p = e % kKT;            // keys: position fastest
+            kv[j] = d < D && p < np ? kt[(int64_t)d * ctx + p0 + p] : 0.f;
+            const int pv = e / kRowsMaxD, dv = e % kRowsMaxD;  // values: dim fastest
+            vv[j] = dv < D && pv < np ? vc[(int64_t)(p0 + pv) * D + dv] : 0.f;
         }
-        for (int e = tid; e < kKT * D; e += kAttThreads) {
-            const int p = e / D, d = e - p * D;
-            vs[p][d] = p < np ? vc[(int64_t)(p0 + p) * D + d] : 0.f;
+#pragma unroll
+        for (int j = 0; j < kRowsMaxD * kKT / kAttThreads; ++j) {
+            const int e = tid + j * kAttThreads;
+            ks[e / kKT][e % kKT] = kv[j];
+            vs[e / kRowsMaxD][e % kRowsMaxD] = vv[j];
         }
         __syncthreads();
         // scores of this tile, masked past each query's own position
-        float s[4];
+        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < D4; d += 4) {
+            const f4 qv = *reinterpret_cast<const f4*>(&qs[sq][d]);
+            const f4 k0 = *reinterpret_cast<const f4*>(&ks[d][4 * sp]);
+            const f4 k1 = *reinterpret_cast<const f4*>(&ks[d + 1][4 * sp]);
+            const f4 k2 = *reinterpret_cast<const f4*>(&ks[d + 2][4 * sp]);
+            const f4 k3 = *reinterpret_cast<const f4*>(&ks[d + 3][4 * sp]);
+            acc += qv.x * k0;   // head dims in order for every score
+            acc += qv.y * k1;
+            acc += qv.z * k2;
+            acc += qv.w * k3;
+        }
+        float s[4] = {acc.x, acc.y, acc.z, acc.w};
         float tmax = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const int p = sp + 16 * j;
-            float acc = 0.f;
-            for (int d = 0; d < D; ++d) acc += qs[sq][d] * ks[d][p];
+            const int p = 4 * sp + j;
             const bool ok = sq < nq && p < np && p0 + p <= pos0 + t0 + sq;
-            s[j] = ok ? acc : -INFINITY;
+            s[j] = ok ? s[j] : -INFINITY;
             tmax = fmaxf(tmax, s[j]);
         }
         // the 16 threads of a query (consecutive lanes) agree on its tile max
@@ -176,31 +233,32 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = m_new == -INFINITY ? 1.f : __expf(m_run - m_new);
         float lsum = 0.f;
+        f4 e4;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float e = s[j] == -INFINITY ? 0.f : __expf(s[j] - m_new);
-            ps[sq][sp + 16 * j] = e;
+            e4[j] = e;
             lsum += e;
         }
+        *reinterpret_cast<f4*>(&ps[sq][4 * sp]) = e4;
         lsum = row16_sum(lsum);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         __syncthreads();
-#pragma unroll
-        for (int j = 0; j < kDPer; ++j) {
-            const int d = og + 16 * j;
-            float acc = o[j] * alpha;
-            if (d < D) {
-                for (int p = 0; p < np; ++p) acc += ps[oq][p] * vs[p][d];
-            }
-            o[j] = acc;
+        o0 *= alpha;
+        o1 *= alpha;
+        for (int p = 0; p < np; ++p) {
+            const float w = ps[oq][p];
+            o0 += w * *reinterpret_cast<const f4*>(&vs[p][4 * og]);
+            o1 += w * *reinterpret_cast<const f4*>(&vs[p][64 + 4 * og]);
         }
     }
     if (oq < nq) {
 #pragma unroll
-        for (int j = 0; j < kDPer; ++j) {
-            const int d = og + 16 * j;
-            if (d < D) store_out(out, out_dtype, (int64_t)(t0 + oq) * C + hd * D + d, o[j] / l_run);
+        for (int j = 0; j < 8; ++j) {
+            const int d = (j < 4 ? 0 : 64) + 4 * og + (j & 3);
+            const float v = j < 4 ? o0[j & 3] : o1[j & 3];
+            if (d < D) store_out(out, out_dtype, (int64_t)(t0 + oq) * C + hd * D + d, v / l_run);
         }
     }
 }
