@@ -288,15 +288,6 @@ void gemv_quad_kernel(QuadArgs a) {
     auto store_pending = [&]() {
         if (pq < 0) return;
         const float r[4] = {pr0, pr1, pr2, pr3};
-#ifdef NB_QUAD_ACC_IS_TOKEN
-        // lane i (< 4) holds row 4q + i; accumulator t holds token t
-        if (lane < 4) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = 4 * pq + lane;
-                if (i < M && row < PP.N) {
-                    const int64_t e = (int64_t)i * PP.N + row;
-#else
         // lane j (< 4) holds token j; accumulator i holds row 4q + i
         if (lane < M) {
 #pragma unroll
@@ -304,7 +295,6 @@ void gemv_quad_kernel(QuadArgs a) {
                 const int row = 4 * pq + i;
                 if (row < PP.N) {
                     const int64_t e = (int64_t)lane * PP.N + row;
-#endif
                     if (a.y_dtype == NB_BF16) {
                         *as_global_mut(static_cast<bf16_bits*>(PP.y) + e) = f32_to_bf16_rne(r[i]);
                     } else if (PP.y_mode == NB_Y_ADD) {
