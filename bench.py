@@ -474,8 +474,9 @@ def bench_decode(dev, n_gen=256):
            "prompt_tokens": 128, "generated_tokens": n_gen, "vocab": cfg.vocab_size,
            "runs": r["runs"], "model_build_s": round(time.time() - t0, 1),
            "engine": "DecodeEngine: the prompt as one batched pass (packed MFMA GEMMs over the "
-                     "128 rows, row kernels for norms / RoPE / causal attention), then one HIP "
-                     "graph of the step's launches replayed per token",
+                     "128 rows, row kernels for norms / RoPE / causal attention; its launches "
+                     "captured in a HIP graph once per prompt length, in the first run, and "
+                     "replayed), then one HIP graph of the step's launches replayed per token",
            "method": "median of 3 runs; each: the prompt pass timed on its own (prompt_ms, "
                      f"which also chooses the first generated token), then {n_gen - 1} graph "
                      "replays timed (tokens_per_s)"}

@@ -224,6 +224,7 @@ class DecodeEngine(_DecoderBase):
                 ops.GemvBatch([(self.act, d_p, d_c, self.x, C, F, add)]),
             ))
         self.graph = None
+        self._prompt_graphs = {}   # prompt length -> (graph, buffers) of the prompt pass
 
     def reset(self, prompt_tokens):
         super().reset(prompt_tokens)
@@ -263,7 +264,7 @@ class DecodeEngine(_DecoderBase):
         self._launch()
 
     @torch.no_grad()
-    def prefill(self, prompt_tokens):
+    def prefill(self, prompt_tokens, graph: bool = True):
         """Feed the whole prompt as one batched pass -- the reference's
         prompt forward over T tokens (generate_torch.py:299-302) -- and choose
         the first generated token: per layer the q|k|v, o, gate|up and down
@@ -274,19 +275,56 @@ class DecodeEngine(_DecoderBase):
         nb_attention_rows, and the norms with their residual adds are
         nb_rmsnorm_rows; the last row's final norm feeds nb_lm_head_argmax.
         Afterwards the state is that of the per-token path after the last
-        prompt token, so run() continues the sequence."""
+        prompt token, so run() continues the sequence.
+
+        ``graph``: the pass's launches are captured once per prompt length
+        (with buffers kept for that length) and replayed, so a prompt costs
+        one graph launch instead of ~9 host launches per layer; False runs
+        them eagerly."""
         prompt = [int(t) for t in prompt_tokens]
         self.reset(prompt)
-        T, C, F, H, D = len(prompt), self.C, self.F, self.H, self.D
+        T = len(prompt)
+        # the last prompt token's head writes tokens_out[T - 1] and leaves
+        # position T, as the per-token path would; no layer reads the state
+        st = _lib.DecodeState(0, T - 1, prompt[-1], T - 1, 0)
+        self.state_t[: ctypes.sizeof(st)].copy_(torch.frombuffer(bytearray(bytes(st)),
+                                                                  dtype=torch.uint8))
+        toks = torch.tensor(prompt, dtype=torch.int32)
+        if not graph:
+            bufs = self._prompt_buffers(T)
+            bufs["toks"].copy_(toks)
+            self._prompt_launches(T, bufs)
+        else:
+            cached = self._prompt_graphs.get(T)
+            if cached is None:
+                if len(self._prompt_graphs) >= 4:   # keep the buffers of a few lengths
+                    self._prompt_graphs.clear()
+                bufs = self._prompt_buffers(T)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    self._prompt_launches(T, bufs)
+                cached = self._prompt_graphs[T] = (g, bufs)
+            g, bufs = cached
+            bufs["toks"].copy_(toks)
+            g.replay()
+        self.fed = T
+
+    def _prompt_buffers(self, T):
+        z, bf16, C, F = self._z, torch.bfloat16, self.C, self.F
+        return {"toks": torch.zeros(T, dtype=torch.int32, device=self.dev),
+                "x": z(T, C), "h": z(T, C, dt=bf16), "qkv": z(T, 3 * C), "q": z(T, C),
+                "att": z(T, C, dt=bf16), "o": z(T, C), "gu": z(T, 2 * F),
+                "act": z(T, F, dt=bf16), "dn": z(T, C)}
+
+    def _prompt_launches(self, T, b):
+        C, F, H, D = self.C, self.F, self.H, self.D
         lib, ck = _lib.load(), _lib.check
         s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
-        z, bf16, BF = self._z, torch.bfloat16, _lib.NB_BF16
-        toks = torch.tensor(prompt, dtype=torch.int32, device=self.dev)
-        x, h = z(T, C), z(T, C, dt=bf16)
-        qkv, q, att, o = z(T, 3 * C), z(T, C), z(T, C, dt=bf16), z(T, C)
-        gu, act, dn = z(T, 2 * F), z(T, F, dt=bf16), z(T, C)
+        BF = _lib.NB_BF16
+        x, h, qkv, q, att, o, gu, act, dn = (b[k] for k in ("x", "h", "qkv", "q", "att", "o",
+                                                              "gu", "act", "dn"))
         ln1 = [n[0] for n in self.norms]
-        ck(lib.nb_rmsnorm_rows(_ptr(x), None, _ptr(self.emb_f32), _ptr(toks), _ptr(ln1[0]),
+        ck(lib.nb_rmsnorm_rows(_ptr(x), None, _ptr(self.emb_f32), _ptr(b["toks"]), _ptr(ln1[0]),
                                _ptr(h), BF, T, C, self.eps, s))
         for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
             ops.gemm_prefill(h, qkv_p, qkv_c, 3 * C, C, out=qkv)
@@ -303,17 +341,10 @@ class DecodeEngine(_DecoderBase):
             w_next = ln1[l + 1] if l + 1 < len(self.fused) else self.ln_f
             ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(dn), None, None, _ptr(w_next), _ptr(h), BF, T,
                                    C, self.eps, s))
-        # the last prompt token's head: its step writes tokens_out[T - 1] and
-        # leaves position T, as the per-token path would
-        st = _lib.DecodeState(0, T - 1, prompt[-1], T - 1, 0)
-        self.state_t[: ctypes.sizeof(st)].copy_(torch.frombuffer(bytearray(bytes(st)),
-                                                                  dtype=torch.uint8))
-        h_last = h[T - 1]
-        ck(lib.nb_lm_head_argmax(_ptr(h_last), _ptr(self.emb_bf16), _ptr(self.logits),
+        ck(lib.nb_lm_head_argmax(_ptr(h[T - 1]), _ptr(self.emb_bf16), _ptr(self.logits),
                                  _ptr(self.state_t), _ptr(self.tokens), self.max_steps,
                                  _ptr(self.force), self.n_force, self.V, C, s))
         self.x.copy_(x[T - 1])
-        self.fed = T
 
     @torch.no_grad()
     def generate(self, prompt_tokens, n_generate: int, batched_prompt: bool = True) -> list:

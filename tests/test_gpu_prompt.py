@@ -253,6 +253,27 @@ def test_prefill_vs_oracle(dev, tiny_model, tiny_ref, T):
     _check_prefill(eng, tiny_ref, seq, 5e-3)
 
 
+def test_prefill_graph_equals_eager(dev, tiny_model):
+    """The prompt pass replayed from its captured graph (buffers kept per
+    prompt length) equals the eager launches bit for bit, also for a second
+    prompt of the same length (new tokens into the same buffers) and after a
+    prompt of another length."""
+    eager = DecodeEngine(tiny_model, max_steps=64)
+    cached = DecodeEngine(tiny_model, max_steps=64)
+    g = torch.Generator().manual_seed(77)
+    for T in (24, 24, 9, 24):
+        seq = torch.randint(0, TINY.vocab_size, (T,), generator=g).tolist()
+        note(f"prefill graph vs eager T={T}")
+        eager.prefill(seq, graph=False)
+        cached.prefill(seq)
+        torch.cuda.synchronize()
+        assert torch.equal(eager.logits, cached.logits)
+        assert torch.equal(eager.x, cached.x)
+        assert torch.equal(eager.kc, cached.kc) and torch.equal(eager.vc, cached.vc)
+        assert eager.state() == cached.state()
+        assert int(eager.tokens[T - 1]) == int(cached.tokens[T - 1])
+
+
 def test_prefill_vs_teacher_forced(dev, tiny_model):
     """The batched prompt leaves the state, caches and logits the per-token
     path leaves after the same prompt, and nothing past the prompt in the
