@@ -379,7 +379,7 @@ struct PrefillPlan {
 // partial products (written, then read once by the reduction) of at most
 // twice the packed weight's bytes, else four times.  Measured on MI355X
 // over the four 2.2B layer shapes: M = 128 layer 140 -> 86 us, M = 512
-// 191 -> 156 us (down 75 -> 44, o 28 -> 24), M = 2048 unchanged (no split);
+// 191 -> 156-162 us (down 75 -> 44-45 us), M = 2048 unchanged (no split);
 // splitting tiles that already fill the grid was slower.
 PrefillPlan prefill_plan(int M, int N, int K, bool allow_split) {
     const int64_t cus = device_cu_count();
