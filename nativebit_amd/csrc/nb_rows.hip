@@ -151,7 +151,7 @@ __global__ void rope_kv_rows_kernel(const float* __restrict__ qkv, float* __rest
 // to a multiple of 4) are zero in LDS, so the dot products run over float4
 // pieces and add exact zeros.
 // ---------------------------------------------------------------------------
-constexpr int kQB = 16;       // queries per workgroup
+constexpr int kQB = 8;        // queries per workgroup (32 threads each)
 constexpr int kKT = 64;       // keys per tile
 constexpr int kAttThreads = 256;
 constexpr int kRowsMaxD = 128;
@@ -176,13 +176,13 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
         const int i = e / kQPitch, d = e - i * kQPitch;
         qs[i][d] = i < nq && d < D ? q[(int64_t)(t0 + i) * C + hd * D + d] : 0.f;
     }
-    // scores: thread (sq, sp) takes query sq and keys 4 sp .. 4 sp + 3
-    const int sq = tid >> 4, sp = tid & 15;
+    typedef __attribute__((ext_vector_type(2))) float f2;
+    // scores: thread (sq, sp) takes query sq and keys 2 sp, 2 sp + 1
+    const int sq = tid >> 5, sp = tid & 31;
     // weighted values: thread (oq, og) takes query oq and dims 4 og .. 4 og + 3
-    // and 64 + 4 og .. 64 + 4 og + 3
-    const int oq = tid >> 4, og = tid & 15;
-    f4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY, l_run = 0.f;  // per query, kept by its 16 threads alike
+    const int oq = tid >> 5, og = tid & 31;
+    f4 o0 = {0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;  // per query, kept by its 32 threads alike
     const int last = pos0 + t0 + nq - 1;  // the last position any query sees
     const float* kt = k_cache + (int64_t)hd * D * ctx;
     const float* vc = v_cache + (int64_t)hd * ctx * D;
@@ -207,58 +207,57 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
         }
         __syncthreads();
         // scores of this tile, masked past each query's own position
-        f4 acc = {0.f, 0.f, 0.f, 0.f};
+        f2 acc = {0.f, 0.f};
         for (int d = 0; d < D4; d += 4) {
             const f4 qv = *reinterpret_cast<const f4*>(&qs[sq][d]);
-            const f4 k0 = *reinterpret_cast<const f4*>(&ks[d][4 * sp]);
-            const f4 k1 = *reinterpret_cast<const f4*>(&ks[d + 1][4 * sp]);
-            const f4 k2 = *reinterpret_cast<const f4*>(&ks[d + 2][4 * sp]);
-            const f4 k3 = *reinterpret_cast<const f4*>(&ks[d + 3][4 * sp]);
+            const f2 k0 = *reinterpret_cast<const f2*>(&ks[d][2 * sp]);
+            const f2 k1 = *reinterpret_cast<const f2*>(&ks[d + 1][2 * sp]);
+            const f2 k2 = *reinterpret_cast<const f2*>(&ks[d + 2][2 * sp]);
+            const f2 k3 = *reinterpret_cast<const f2*>(&ks[d + 3][2 * sp]);
             acc += qv.x * k0;   // head dims in order for every score
             acc += qv.y * k1;
             acc += qv.z * k2;
             acc += qv.w * k3;
         }
-        float s[4] = {acc.x, acc.y, acc.z, acc.w};
+        float s[2] = {acc.x, acc.y};
         float tmax = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int p = 4 * sp + j;
+        for (int j = 0; j < 2; ++j) {
+            const int p = 2 * sp + j;
             const bool ok = sq < nq && p < np && p0 + p <= pos0 + t0 + sq;
             s[j] = ok ? s[j] : -INFINITY;
             tmax = fmaxf(tmax, s[j]);
         }
-        // the 16 threads of a query (consecutive lanes) agree on its tile max
+        // the 32 threads of a query (consecutive lanes, two rows of 16)
+        // agree on its tile max
         tmax = row16_max(tmax);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
         const float m_new = fmaxf(m_run, tmax);
         const float alpha = m_new == -INFINITY ? 1.f : __expf(m_run - m_new);
         float lsum = 0.f;
-        f4 e4;
+        f2 e2;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < 2; ++j) {
             const float e = s[j] == -INFINITY ? 0.f : __expf(s[j] - m_new);
-            e4[j] = e;
+            e2[j] = e;
             lsum += e;
         }
-        *reinterpret_cast<f4*>(&ps[sq][4 * sp]) = e4;
+        *reinterpret_cast<f2*>(&ps[sq][2 * sp]) = e2;
         lsum = row16_sum(lsum);
+        lsum += __shfl_xor(lsum, 16);
         l_run = l_run * alpha + lsum;
         m_run = m_new;
         __syncthreads();
         o0 *= alpha;
-        o1 *= alpha;
         for (int p = 0; p < np; ++p) {
-            const float w = ps[oq][p];
-            o0 += w * *reinterpret_cast<const f4*>(&vs[p][4 * og]);
-            o1 += w * *reinterpret_cast<const f4*>(&vs[p][64 + 4 * og]);
+            o0 += ps[oq][p] * *reinterpret_cast<const f4*>(&vs[p][4 * og]);
         }
     }
     if (oq < nq) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int d = (j < 4 ? 0 : 64) + 4 * og + (j & 3);
-            const float v = j < 4 ? o0[j & 3] : o1[j & 3];
-            if (d < D) store_out(out, out_dtype, (int64_t)(t0 + oq) * C + hd * D + d, v / l_run);
+        for (int j = 0; j < 4; ++j) {
+            const int d = 4 * og + j;
+            if (d < D) store_out(out, out_dtype, (int64_t)(t0 + oq) * C + hd * D + d, o0[j] / l_run);
         }
     }
 }
