@@ -131,22 +131,6 @@ int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* packed,
                           int K, void* workspace, int64_t ws_bytes, void* stream);
 
 /*
- * nb_gemm_prefill with a caller workspace (>= nb_gemm_prefill_ws_bytes(M, N,
- * K) bytes, 256-byte aligned, contents clobbered): W is expanded to bf16 in
- * the workspace by the format kernel and y = x . W^T is one hipBLASLt GEMM
- * (bf16 operands, fp32 accumulation) -- faster than the fused kernel for
- * many activation rows.  Same operands and result contract as
- * nb_gemm_prefill; the fused kernel runs where the library has no algorithm.
- * Replaces: the same batched branch of PackedLinear.forward in its bf16
- *           form (inference/triton_kernel.py:258-275, inference/eval_ppl.py:
- *           149-174: gather W, cast to bf16, dense matmul).
- */
-int64_t nb_gemm_prefill_ws_bytes(int M, int N, int K);
-int nb_gemm_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
-                       void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
-                       int64_t ws_bytes, void* stream);
-
-/*
  * Unpack `count` indices of `bits` bits to one byte each.
  * Replaces: unpack_3bit / unpack_4bit / unpack_nbits
  *           (nativebit/pack.py:44-68, 85-90, 119-138) and
@@ -412,16 +396,20 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
  * step (keys [n_head][head_dim][ctx], values [n_head][ctx][head_dim], fp32).
  * ------------------------------------------------------------------------ */
 /*
- * Per row t < T: with emb and tokens, x[t] = emb[tokens[t]] (the embedding
- * lookup); with add, x[t] += add[t] (a residual add); then h[t] =
- * (x[t] / sqrt(mean(x[t]^2) + eps)) * w (C wide; x, add, emb, w fp32; h
- * NB_F32 or NB_BF16).  x is updated in place.
+ * Per row t < T: with emb (vocab rows of C) and tokens, x[t] =
+ * emb[tokens[t]] (the embedding lookup); with add, x[t] += add[t] (a
+ * residual add); then h[t] = (x[t] / sqrt(mean(x[t]^2) + eps)) * w (C wide;
+ * x, add, emb, w fp32; h NB_F32 or NB_BF16).  x is updated in place.  A
+ * token outside [0, vocab) reads no memory: its rows of x and h are set to
+ * NaN (the reference's lookup raises; a kernel cannot).  vocab is ignored
+ * without emb.
  * Replaces: RMSNorm.forward over a sequence (inference/generate_torch.py:
  *           29-38) with the residual adds of TransformerBlock.forward
  *           (128-132) and the embedding lookup of PackedGPT.forward (150).
  */
 int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
-                    const float* w, void* h, int h_dtype, int T, int C, float eps, void* stream);
+                    int vocab, const float* w, void* h, int h_dtype, int T, int C, float eps,
+                    void* stream);
 /*
  * act[t][i] = silu(gu[t][2i]) * gu[t][2i+1] for i < F (gu: T rows of 2F fp32,
  * gate and up interleaved by column, as a gate|up layer with alternating

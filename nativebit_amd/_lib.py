@@ -68,15 +68,13 @@ SIGNATURES = {
     "nb_gemm_prefill": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P]),
     "nb_gemm_prefill_split_ws_bytes": (_L, [_I, _I, _I]),
     "nb_gemm_prefill_split": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P, _L, _P]),
-    "nb_gemm_prefill_ws_bytes": (_L, [_I, _I, _I]),
-    "nb_gemm_prefill_ws": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P, _L, _P]),
     "nb_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P]),
     "nb_attention_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "nb_attention_work_floats": (_I, [_I]),
     "nb_attention_step_static": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "nb_attention_static_scratch_bytes": (_L, []),
     "nb_silu_mul": (_I, [_P, _P, _I, _I, _P]),
-    "nb_rmsnorm_rows": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, ctypes.c_float, _P]),
+    "nb_rmsnorm_rows": (_I, [_P, _P, _P, _P, _I, _P, _P, _I, _I, _I, ctypes.c_float, _P]),
     "nb_silu_pairs_rows": (_I, [_P, _P, _I, _I, _I, _P]),
     "nb_rope_kv_rows": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _I, _I, _I, _P]),
     "nb_attention_rows": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P]),

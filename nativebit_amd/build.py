@@ -19,7 +19,6 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(CSRC, "_build")
 LIB = os.path.join(HERE, "libnativebit_amd.so")
 ARCH = "gfx950"
-ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 COMMON = [
     f"--offload-arch={ARCH}",
@@ -65,8 +64,7 @@ def build(verbose: bool = True) -> str:
     with concurrent.futures.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = LIB + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs + [
-        "-L", os.path.join(ROCM, "lib"), "-lhipblaslt", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -612,7 +612,8 @@ int nb_attention_step_static(const float* qkv, float* k_cache, float* v_cache, c
 int64_t nb_attention_static_scratch_bytes(void) { return static_attention_scratch_bytes(); }
 
 int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
-                    const float* w, void* h, int h_dtype, int T, int C, float eps, void* stream) {
+                    int vocab, const float* w, void* h, int h_dtype, int T, int C, float eps,
+                    void* stream) {
     const char* fn = "nb_rmsnorm_rows";
     if (T < 0 || C < 1) return fail(NB_EINVAL, "%s: T=%d C=%d", fn, T, C);
     if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(NB_EINVAL, "%s: eps=%g", fn, (double)eps);
@@ -622,6 +623,7 @@ int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t*
         return fail(NB_EINVAL, "%s: emb and tokens go together", fn);
     }
     if (emb && add) return fail(NB_EINVAL, "%s: an embedding lookup takes no add", fn);
+    if (emb && vocab < 1) return fail(NB_EINVAL, "%s: vocab=%d rows in the embedding", fn, vocab);
     if (!aligned(x, 4) || !aligned(w, 4) || (add && !aligned(add, 4)) || (emb && !aligned(emb, 4)) ||
         (tokens && !aligned(tokens, 4)) || !aligned(h, dtype_size(h_dtype))) {
         return fail(NB_EALIGN, "%s: misaligned pointer", fn);
@@ -629,7 +631,7 @@ int nb_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t*
     if (T == 0) return NB_OK;
     int st = ensure_device();
     if (st) return st;
-    return launch_rmsnorm_rows(x, add, emb, tokens, w, h, h_dtype, T, C, eps,
+    return launch_rmsnorm_rows(x, add, emb, tokens, vocab, w, h, h_dtype, T, C, eps,
                                static_cast<hipStream_t>(stream));
 }
 
@@ -805,39 +807,6 @@ extern "C" int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* 
     return launch_prefill2(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K,
                            need > 0 ? workspace : nullptr, ws_bytes,
                            static_cast<hipStream_t>(stream));
-}
-
-extern "C" int64_t nb_gemm_prefill_ws_bytes(int M, int N, int K) {
-    (void)M;
-    if (N < 0 || K < 0) return 0;
-    return prefill_ws_weight_bytes(N, K) + kPrefillBlasWorkspace;
-}
-
-extern "C" int nb_gemm_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed,
-                                  const float* codebook, void* y, int y_dtype, int64_t ldy, int M,
-                                  int N, int K, void* workspace, int64_t ws_bytes, void* stream) {
-    const char* fn = "nb_gemm_prefill_ws";
-    if (M < 0 || N < 0 || K < 0) return fail(NB_EINVAL, "%s: negative shape", fn);
-    if (K % 128 != 0) return fail(NB_EUNSUPPORTED, "%s: K=%d not a multiple of 128", fn, K);
-    if ((int64_t)N * (K / 128) >= (1LL << 31)) return fail(NB_EUNSUPPORTED, "%s: too many blocks", fn);
-    if (y_dtype != NB_F32 && y_dtype != NB_BF16) return fail(NB_EINVAL, "%s: y_dtype=%d", fn, y_dtype);
-    if (M == 0 || N == 0) return NB_OK;
-    if (K == 0) return fail(NB_EUNSUPPORTED, "%s: K == 0 (use nb_gemv)", fn);
-    if (ldx < K || ldy < N) return fail(NB_EINVAL, "%s: ldx=%lld < K or ldy=%lld < N", fn,
-                                        (long long)ldx, (long long)ldy);
-    if (!x || !packed || !codebook || !y || !workspace) return fail(NB_EINVAL, "%s: NULL pointer", fn);
-    if (!aligned(x, 16) || ldx % 8 != 0) return fail(NB_EALIGN, "%s: x must be 16-byte aligned with ldx %% 8 == 0", fn);
-    if (!aligned(packed, 8) || !aligned(codebook, 16)) return fail(NB_EALIGN, "%s: packed 8- / codebook 16-byte alignment", fn);
-    if (!aligned(y, dtype_size(y_dtype))) return fail(NB_EALIGN, "%s: y not aligned to its dtype", fn);
-    if (!aligned(workspace, 256)) return fail(NB_EALIGN, "%s: workspace not 256-byte aligned", fn);
-    if (ws_bytes < nb_gemm_prefill_ws_bytes(M, N, K)) {
-        return fail(NB_EINVAL, "%s: workspace of %lld bytes < %lld", fn, (long long)ws_bytes,
-                    (long long)nb_gemm_prefill_ws_bytes(M, N, K));
-    }
-    int st = ensure_device();
-    if (st) return st;
-    return launch_prefill_ws(x, ldx, packed, codebook, y, y_dtype, ldy, M, N, K, workspace,
-                             ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 namespace {

@@ -137,18 +137,6 @@ int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const flo
                     int64_t ws_bytes, hipStream_t stream);
 int64_t prefill_split_bytes(int M, int N, int K);
 
-// hipBLASLt's own share of the prefill workspace, after the bf16 weight.
-constexpr int64_t kPrefillBlasWorkspace = 32ll << 20;
-
-// Bytes of the bf16 weight copy at the start of the prefill workspace.
-int64_t prefill_ws_weight_bytes(int N, int K);
-
-// Dequantize W to bf16 in the workspace, then one hipBLASLt GEMM (the fused
-// kernel if the library has no algorithm for the shape).
-int launch_prefill_ws(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
-                      void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
-                      int64_t ws_bytes, hipStream_t stream);
-
 // Decode-step kernels (nb_decode.hip).
 int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,
                        const float* w, void* h, int h_dtype, int n, float eps, hipStream_t stream);
@@ -169,7 +157,7 @@ int64_t static_attention_scratch_bytes();
 
 // Batched-pass kernels (nb_rows.hip); arguments validated.
 int launch_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
-                        const float* w, void* h, int h_dtype, int T, int C, float eps,
+                        int vocab, const float* w, void* h, int h_dtype, int T, int C, float eps,
                         hipStream_t stream);
 int launch_silu_pairs_rows(const float* gu, void* act, int act_dtype, int T, int F,
                            hipStream_t stream);

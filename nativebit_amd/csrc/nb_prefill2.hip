@@ -304,7 +304,9 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
             const f32x4_t v = acc[i][j];
             if (y_dtype == NB_BF16) {
                 bf16_bits* yp = static_cast<bf16_bits*>(yb) + (int64_t)m * ldy + n;
-                if (n + 3 < a.N && ((ldy | n) & 3) == 0) {
+                // one 8-byte store where the four outputs exist and the
+                // address allows it (y may be any 2-byte-aligned view)
+                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
                     u32x2_t p;
                     p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
                     p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
                 }
             } else {
                 float* yp = static_cast<float*>(yb) + (int64_t)m * ldy + n;
-                if (n + 3 < a.N && ((ldy | n) & 3) == 0) {
+                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
                     *reinterpret_cast<f32x4_t*>(yp) = v;
                 } else {
 #pragma unroll
@@ -336,7 +338,12 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
                                                              int S, int M, int N, void* y,
                                                              int y_dtype, int64_t ldy) {
     const int64_t plane = (int64_t)M * N;
-    const bool vec = ((N | ldy) & 3) == 0;
+    // four outputs a thread where every row starts on a 4-output boundary
+    // of both part and y (rows of 4k outputs, bases aligned for the vector
+    // width: 16 bytes for part and fp32 y, 8 for bf16 y)
+    const uintptr_t y_align = y_dtype == NB_BF16 ? 7 : 15;
+    const bool vec = ((N | ldy) & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & y_align) == 0 &&
+                     (reinterpret_cast<uintptr_t>(part) & 15) == 0;
     const int64_t total = vec ? plane / 4 : plane;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * 256) {

@@ -41,12 +41,22 @@ constexpr int kNormRegs = 16;      // elements per thread kept in registers (C <
 
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_rows_kernel(
     float* __restrict__ x, const float* __restrict__ add, const float* __restrict__ emb,
-    const int32_t* __restrict__ tokens, const float* __restrict__ w, void* __restrict__ h,
-    int h_dtype, int C, float eps) {
+    const int32_t* __restrict__ tokens, int vocab, const float* __restrict__ w,
+    void* __restrict__ h, int h_dtype, int C, float eps) {
     __shared__ float red[kNormThreads / 64];
     const int t = blockIdx.x;
     float* xr = x + (int64_t)t * C;
-    const float* src = tokens ? emb + (int64_t)tokens[t] * C : nullptr;
+    const int tok = tokens ? tokens[t] : 0;
+    if (tokens && (tok < 0 || tok >= vocab)) {
+        // a token outside the table reads nothing: its row of x and h is NaN
+        // (the whole workgroup leaves here, before any barrier)
+        for (int i = threadIdx.x; i < C; i += kNormThreads) {
+            xr[i] = __builtin_nanf("");
+            store_out(h, h_dtype, (int64_t)t * C + i, __builtin_nanf(""));
+        }
+        return;
+    }
+    const float* src = tokens ? emb + (int64_t)tok * C : nullptr;
     const float* ar = add ? add + (int64_t)t * C : nullptr;
     // rows of up to kNormRegs * 256 elements stay in registers between the
     // sum of squares and the scaling, with every load issued up front
@@ -265,10 +275,10 @@ __global__ __launch_bounds__(kAttThreads) void attention_rows_kernel(
 }  // namespace
 
 int launch_rmsnorm_rows(float* x, const float* add, const float* emb, const int32_t* tokens,
-                        const float* w, void* h, int h_dtype, int T, int C, float eps,
+                        int vocab, const float* w, void* h, int h_dtype, int T, int C, float eps,
                         hipStream_t stream) {
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(T), dim3(kNormThreads), 0, stream, x, add, emb,
-                       tokens, w, h, h_dtype, C, eps);
+                       tokens, vocab, w, h, h_dtype, C, eps);
     return check_launch("nb_rmsnorm_rows");
 }
 

@@ -324,8 +324,8 @@ class DecodeEngine(_DecoderBase):
         x, h, qkv, q, att, o, gu, act, dn = (b[k] for k in ("x", "h", "qkv", "q", "att", "o",
                                                               "gu", "act", "dn"))
         ln1 = [n[0] for n in self.norms]
-        ck(lib.nb_rmsnorm_rows(_ptr(x), None, _ptr(self.emb_f32), _ptr(b["toks"]), _ptr(ln1[0]),
-                               _ptr(h), BF, T, C, self.eps, s))
+        ck(lib.nb_rmsnorm_rows(_ptr(x), None, _ptr(self.emb_f32), _ptr(b["toks"]), self.V,
+                               _ptr(ln1[0]), _ptr(h), BF, T, C, self.eps, s))
         for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
             ops.gemm_prefill(h, qkv_p, qkv_c, 3 * C, C, out=qkv)
             ck(lib.nb_rope_kv_rows(_ptr(qkv), _ptr(self.kc[l]), _ptr(self.vc[l]), _ptr(self.cos),
@@ -333,14 +333,14 @@ class DecodeEngine(_DecoderBase):
             ck(lib.nb_attention_rows(_ptr(q), _ptr(self.kc[l]), _ptr(self.vc[l]), 0, T, _ptr(att),
                                      BF, H, D, self.ctx, s))
             ops.gemm_prefill(att, o_p, o_c, C, C, out=o)
-            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(o), None, None, _ptr(self.norms[l][1]), _ptr(h),
-                                   BF, T, C, self.eps, s))
+            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(o), None, None, 0, _ptr(self.norms[l][1]),
+                                   _ptr(h), BF, T, C, self.eps, s))
             ops.gemm_prefill(h, gu_p, gu_c, 2 * F, C, out=gu)  # gate, up columns interleaved
             ck(lib.nb_silu_pairs_rows(_ptr(gu), _ptr(act), BF, T, F, s))
             ops.gemm_prefill(act, d_p, d_c, C, F, out=dn)
             w_next = ln1[l + 1] if l + 1 < len(self.fused) else self.ln_f
-            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(dn), None, None, _ptr(w_next), _ptr(h), BF, T,
-                                   C, self.eps, s))
+            ck(lib.nb_rmsnorm_rows(_ptr(x), _ptr(dn), None, None, 0, _ptr(w_next), _ptr(h), BF,
+                                   T, C, self.eps, s))
         ck(lib.nb_lm_head_argmax(_ptr(h[T - 1]), _ptr(self.emb_bf16), _ptr(self.logits),
                                  _ptr(self.state_t), _ptr(self.tokens), self.max_steps,
                                  _ptr(self.force), self.n_force, self.V, C, s))

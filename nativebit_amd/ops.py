@@ -300,10 +300,8 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
     the packed weight dequantized into LDS tiles; a layer whose tile grid
     would leave CUs idle -- few tokens, narrow layers -- is split over K
     ranges, with fp32 partial products in a workspace taken from torch's
-    allocator and one reduction launch), "fused" (nb_gemm_prefill: the same
-    kernel in one launch over all of K, no workspace), or "blas"
-    (nb_gemm_prefill_ws: W expanded to bf16 in a workspace, then one
-    hipBLASLt GEMM -- kept as a comparison)."""
+    allocator and one reduction launch) or "fused" (nb_gemm_prefill: the same
+    kernel in one launch over all of K, no workspace)."""
     for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
         _require_cuda(name, t)
     _same_device(x, packed, codebook)
@@ -320,16 +318,9 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
         out = torch.empty((M, N), dtype=out_dtype, device=x.device)
     elif out.shape != (M, N) or out.dtype not in _DT or out.stride(1) != 1:
         raise ValueError("out must be (M, N), row-contiguous")
-    if path not in ("auto", "fused", "blas"):
+    if path not in ("auto", "fused"):
         raise ValueError(f"unknown prefill path {path!r}")
     lib = _lib.load()
-    if path == "blas":
-        nbytes = int(lib.nb_gemm_prefill_ws_bytes(M, N, K))
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
-        _lib.check(lib.nb_gemm_prefill_ws(
-            x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
-            _DT[out.dtype], out.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x)))
-        return out
     if path == "auto":
         nbytes = int(lib.nb_gemm_prefill_split_ws_bytes(M, N, K))
         ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device) if nbytes else None
@@ -371,8 +362,10 @@ def pack(indices: torch.Tensor, bits: int) -> torch.Tensor:
 
 
 def dequant(packed: torch.Tensor, codebook: torch.Tensor, total: int, bits: int,
-            block_size: int, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
-    """Flat W[:total] = codebook[i // block_size][index i] (device)."""
+            block_size: int, out_dtype: torch.dtype = torch.float32,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Flat W[:total] = codebook[i // block_size][index i] (device); into
+    ``out`` (contiguous, >= total elements of out_dtype) when given."""
     _require_cuda("packed", packed)
     _require_cuda("codebook", codebook)
     _same_device(packed, codebook)
@@ -384,7 +377,14 @@ def dequant(packed: torch.Tensor, codebook: torch.Tensor, total: int, bits: int,
         raise ValueError("packed stream too short for total weights")
     if out_dtype not in _DT:
         raise TypeError(f"out_dtype {out_dtype} not supported")
-    w = torch.empty(total, dtype=out_dtype, device=packed.device)
+    if out is None:
+        w = torch.empty(total, dtype=out_dtype, device=packed.device)
+    else:
+        if (out.dtype != out_dtype or not out.is_contiguous() or out.numel() < total
+                or out.device != packed.device):
+            raise ValueError(f"out must be a contiguous {out_dtype} tensor of >= {total} "
+                             "elements on the stream's device")
+        w = out
     _lib.check(_lib.load().nb_dequant(
         packed.data_ptr(), codebook.data_ptr(), w.data_ptr(), _DT[out_dtype], total,
         codebook.shape[0], bits, codebook.shape[1], block_size, _stream(packed)))

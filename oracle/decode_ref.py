@@ -139,9 +139,8 @@ class DecoderRef:
         (rounded back to fp32): the spread between the two is the rounding
         noise a different fp32 summation order leaves in the logits."""
         c = self.cfg
-        H, D = c.n_head, self.D
         x = self.emb[idx]
-        B, T, C = x.shape
+        T = x.shape[1]
 
         def lin(v, w):
             if isinstance(w, PackedRef):
@@ -154,41 +153,79 @@ class DecoderRef:
                 return (v.to(accum_dtype) @ w.to(accum_dtype).T).float()
             return v @ w.T
 
+        p0 = pos0 if cache is None else cache[1]
         for l, L in enumerate(self.layers):
-            h = rmsnorm(x, self.norms[l][0], c.norm_eps)
-            q, k, v = lin(h, L["qkv"]).chunk(3, dim=-1)
-            q = q.reshape(B, T, H, D).transpose(1, 2)
-            k = k.reshape(B, T, H, D).transpose(1, 2)
-            v = v.reshape(B, T, H, D).transpose(1, 2)
-            p0 = pos0 if cache is None else cache[1]
-            q, k = rope(q, self.cos, self.sin, p0), rope(k, self.cos, self.sin, p0)
-            if cache is not None:
-                kb, vb = cache[0][l]
-                kb[:, :, p0:p0 + T] = k
-                vb[:, :, p0:p0 + T] = v
-                n = p0 + T
-                att = (q * D ** -0.5) @ kb.transpose(-1, -2)
-                qp = p0 + torch.arange(T)
-                kp = torch.arange(kb.shape[2])
-                mask = (kp[None, :] <= qp[:, None]) & (kp[None, :] < n)
-                att = att.masked_fill(~mask[None, None], torch.finfo(att.dtype).min)
-                o = F.softmax(att, dim=-1) @ vb
-            else:
-                att = (q * D ** -0.5) @ k.transpose(-1, -2)
-                mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
-                att = att.masked_fill(~mask[None, None], float("-inf"))
-                o = F.softmax(att, dim=-1) @ v
-            x = x + lin(o.transpose(1, 2).reshape(B, T, C), L["out_proj"])
-            h2 = rmsnorm(x, self.norms[l][1], c.norm_eps)
-            x = x + lin(F.silu(lin(h2, L["gate"])) * lin(h2, L["up"]), L["down"])
+            kv = cache[0][l] if cache is not None else None
+            x = self.block(l, x, lin, lambda h: self.attention(h, L, lin, kv, p0))
         if cache is not None:
             cache = (cache[0], cache[1] + T)
         x = rmsnorm(x, self.ln_f, c.norm_eps)
         e = self.emb
         if head_dtype is not None:
             x, e = x.to(head_dtype).float(), e.to(head_dtype).float()
-        logits = 30.0 * torch.tanh((x @ e.T) / 30.0)
-        return logits, cache
+        return self.head(x, e), cache
+
+    # -- the pieces of a block, one method each (generate_torch.py:63-162) --
+
+    def block(self, l, x, lin, attend):
+        """x + attn(ln1(x)), then that + ffn(ln2(that))
+        (TransformerBlock.forward, generate_torch.py:128-132)."""
+        eps = self.cfg.norm_eps
+        x = x + attend(rmsnorm(x, self.norms[l][0], eps))
+        h2 = rmsnorm(x, self.norms[l][1], eps)
+        return x + self.ffn(h2, self.layers[l], lin)
+
+    def split_qkv(self, qkv):
+        """q, k, v (B, H, T, D) from the fused projection's output (B, T, 3C):
+        thirds in the order q | k | v, each split into heads
+        (generate_torch.py:74-78)."""
+        B, T, _ = qkv.shape
+        H, D = self.cfg.n_head, self.D
+        q, k, v = qkv.chunk(3, dim=-1)
+        return tuple(t.reshape(B, T, H, D).transpose(1, 2) for t in (q, k, v))
+
+    def rotate(self, x, p0):
+        """RoPE at positions p0 .. p0 + T - 1 (generate_torch.py:48-60)."""
+        return rope(x, self.cos, self.sin, p0)
+
+    def attention(self, h, L, lin, kv, p0):
+        """out_proj of causal softmax attention of the normed input h (B, T,
+        C): with a cache kv = (keys, values) of (B, H, ctx, D) the rotated
+        keys and the values are written at p0 .. p0 + T - 1 and every query
+        sees the cache up to its own position (generate_torch.py:80-95);
+        without one the T tokens attend to each other (the causal
+        scaled_dot_product_attention branch, 97-101)."""
+        B, T, C = h.shape
+        D = self.D
+        q, k, v = self.split_qkv(lin(h, L["qkv"]))
+        q, k = self.rotate(q, p0), self.rotate(k, p0)
+        if kv is not None:
+            kb, vb = kv
+            kb[:, :, p0:p0 + T] = k
+            vb[:, :, p0:p0 + T] = v
+            n = p0 + T
+            att = (q * D ** -0.5) @ kb.transpose(-1, -2)
+            qp = p0 + torch.arange(T)
+            kp = torch.arange(kb.shape[2])
+            mask = (kp[None, :] <= qp[:, None]) & (kp[None, :] < n)
+            att = att.masked_fill(~mask[None, None], torch.finfo(att.dtype).min)
+            o = F.softmax(att, dim=-1) @ vb
+        else:
+            att = (q * D ** -0.5) @ k.transpose(-1, -2)
+            mask = torch.tril(torch.ones(T, T, dtype=torch.bool))
+            att = att.masked_fill(~mask[None, None], float("-inf"))
+            o = F.softmax(att, dim=-1) @ v
+        return lin(o.transpose(1, 2).reshape(B, T, C), L["out_proj"])
+
+    def ffn(self, h2, L, lin):
+        """down(silu(gate(h2)) * up(h2)) (SwiGLU.forward, generate_torch.py:
+        116-117)."""
+        return lin(F.silu(lin(h2, L["gate"])) * lin(h2, L["up"]), L["down"])
+
+    def head(self, x, e):
+        """Tied head with the soft cap: 30 tanh((x e^T) / 30)
+        (generate_torch.py:158-160)."""
+        return 30.0 * torch.tanh((x @ e.T) / 30.0)
 
     def dense_layer(self, l, weight_dtype=None):
         """Block l's linears as dense fp32 weights (rounded through
@@ -228,7 +265,7 @@ class DecoderRef:
         o = (F.softmax(att, dim=-1) @ vals).reshape(H * D)
         x1 = x + lin(o, W["out_proj"])
         h2 = rmsnorm(x1, ln2, c.norm_eps)
-        x2 = x1 + lin(F.silu(lin(h2, W["gate"])) * lin(h2, W["up"]), W["down"])
+        x2 = x1 + self.ffn(h2, W, lin)
         return x2, k[:, 0], v[:, 0]
 
     @torch.no_grad()

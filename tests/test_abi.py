@@ -324,43 +324,6 @@ def test_prefill_empty_is_ok():
     assert prefill(M=0) == _lib.NB_OK and prefill(N=0) == _lib.NB_OK
 
 
-def prefill_ws(**kw):
-    lib = _lib.load()
-    a = dict(x=FAKE, ldx=256, packed=FAKE, codebook=FAKE, y=FAKE, y_dtype=_lib.NB_BF16, ldy=64,
-             M=32, N=64, K=256, ws=FAKE, ws_bytes=int(lib.nb_gemm_prefill_ws_bytes(32, 64, 256)),
-             stream=None)
-    a.update(kw)
-    return lib.nb_gemm_prefill_ws(*a.values())
-
-
-def test_prefill_ws_bytes():
-    lib = _lib.load()
-    # the bf16 copy of W (256-byte rounded) plus the library GEMM's 32 MiB
-    assert lib.nb_gemm_prefill_ws_bytes(32, 64, 256) == 64 * 256 * 2 + (32 << 20)
-    assert lib.nb_gemm_prefill_ws_bytes(1, 3, 100 * 128) == 3 * 100 * 128 * 2 + (32 << 20)
-    assert lib.nb_gemm_prefill_ws_bytes(1, 1, 128 * 3) == 768 + (32 << 20)
-    assert lib.nb_gemm_prefill_ws_bytes(1, 1, 128) == 256 + (32 << 20)
-
-
-@pytest.mark.parametrize("kw,status", [
-    (dict(K=200), _lib.NB_EUNSUPPORTED),
-    (dict(M=-1), _lib.NB_EINVAL),
-    (dict(ldx=128), _lib.NB_EINVAL),
-    (dict(y_dtype=7), _lib.NB_EINVAL),
-    (dict(ws=None), _lib.NB_EINVAL),
-    (dict(ws=FAKE + 16), _lib.NB_EALIGN),
-    (dict(ws_bytes=1 << 20), _lib.NB_EINVAL),
-    (dict(x=FAKE + 8), _lib.NB_EALIGN),
-])
-def test_prefill_ws_validation(kw, status):
-    assert prefill_ws(**kw) == status
-    assert _lib.last_error().startswith("nb_gemm_prefill_ws")
-
-
-def test_prefill_ws_empty_is_ok():
-    assert prefill_ws(M=0) == _lib.NB_OK and prefill_ws(N=0) == _lib.NB_OK
-
-
 def prefill_split(**kw):
     lib = _lib.load()
     a = dict(x=FAKE, ldx=2560, packed=FAKE, codebook=FAKE, y=FAKE, y_dtype=_lib.NB_BF16,
@@ -550,3 +513,25 @@ def test_decode_struct_layout():
     # the ctypes mirrors of struct nb_decode_layer / nb_decode_model
     assert ctypes.sizeof(_lib.DecodeLayer) == 12 * 8
     assert _lib.DecodeModel.layers.offset == 32 and ctypes.sizeof(_lib.DecodeModel) == 32 + 6 * 8
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(vocab=0), _lib.NB_EINVAL),          # a lookup needs the table's row count
+    (dict(vocab=-5), _lib.NB_EINVAL),
+    (dict(tokens=None), _lib.NB_EINVAL),      # emb and tokens go together
+    (dict(add=FAKE), _lib.NB_EINVAL),         # a lookup takes no add
+    (dict(C=0), _lib.NB_EINVAL),
+    (dict(h_dtype=9), _lib.NB_EINVAL),
+    (dict(tokens=FAKE + 2), _lib.NB_EALIGN),
+])
+def test_rmsnorm_rows_validation(kw, status):
+    a = dict(x=FAKE, add=None, emb=FAKE, tokens=FAKE, vocab=11, w=FAKE, h=FAKE,
+             h_dtype=_lib.NB_F32, T=4, C=256, eps=1e-6, stream=None)
+    a.update(kw)
+    assert _lib.load().nb_rmsnorm_rows(*a.values()) == status
+    assert _lib.last_error().startswith("nb_rmsnorm_rows")
+
+
+def test_rmsnorm_rows_vocab_ignored_without_lookup():
+    assert _lib.load().nb_rmsnorm_rows(FAKE, None, None, None, 0, FAKE, FAKE, _lib.NB_F32, 0,
+                                       256, 1e-6, None) == _lib.NB_OK
