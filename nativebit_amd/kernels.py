@@ -22,11 +22,13 @@ from .linear import BS, NE, PackedLinear  # noqa: F401
 
 
 def _as_gemv_input(x: torch.Tensor) -> torch.Tensor:
-    """x as the kernels take it: fp32 or bf16 as given, any other float type
-    cast to fp32 on the device (the reference's kernels load x as fp32,
-    triton_kernel.py:46, 174)."""
+    """x as fp32 on the device, whatever float type it arrives in: the
+    reference's kernels multiply x read as fp32 by the exact fp32 codebook
+    values (triton_kernel.py:46, 174-183; the CUDA kernel takes fp32 x only,
+    cuda_kernel.py:74-77, 97), so these entry points compute exactly that
+    (the fp32 kernels of nb_gemv) for bf16 and fp16 x too."""
     x = x.reshape(-1)
-    return x if x.dtype in (torch.float32, torch.bfloat16) else x.to(torch.float32)
+    return x if x.dtype == torch.float32 else x.to(torch.float32)
 
 
 def dequant_matvec_3bit(x: torch.Tensor, packed_indices: torch.Tensor,

@@ -7,12 +7,16 @@ float32), the same ``out_features`` / ``in_features`` attributes, the same
 a ``forward`` that takes any leading dimensions and returns float32 by
 default.  Differences, all deliberate:
 
-* up to 16 rows run the fused dequant-GEMV kernels; more rows of bf16
-  activations run the packed MFMA prefill kernels, and other batched inputs
-  (fp32 x, other formats) gather W on the device with the format kernel and
-  multiply it densely, as the reference's batched branch does; nothing falls
-  back silently -- a failure raises NativeBitError (the reference swallows
-  every exception, triton_kernel.py:252);
+* up to 16 rows run the fused dequant-GEMV kernels with x read as fp32 and
+  the exact fp32 codebook values (the reference's batch-1 arithmetic, for
+  bf16 and fp16 x too); more rows of bf16 activations run the packed MFMA
+  prefill kernels (bf16-rounded codebook values, the reference's bf16 path
+  of eval_ppl.py:149-174 -- its fp32 batched branch rejects bf16 x), and
+  other batched inputs (fp32 x, other formats) gather W on the device with
+  the format kernel and multiply it densely, as the reference's batched
+  branch does; nothing falls back silently -- a failure raises
+  NativeBitError (the reference swallows every exception,
+  triton_kernel.py:252);
 * bit width, entries per block and block size are attributes (defaults 3, 8
   and 128, the reference's constants, triton_kernel.py:18-19);
 * ``out_dtype`` may be bfloat16 for callers that keep activations in bf16.
@@ -68,11 +72,13 @@ class PackedLinear(torch.nn.Module):
         if x.dim() == 0 or shape[-1] != self.in_features:
             raise ValueError(f"x last dim must be {self.in_features}, got {tuple(shape)}")
         x_flat = x.reshape(-1, self.in_features)
-        if x_flat.dtype not in (torch.float32, torch.bfloat16):
-            # any other float type is read as fp32, as the reference's kernels
-            # load x (.to(tl.float32), triton_kernel.py:46, 174)
-            x_flat = x_flat.to(torch.float32)
         M = x_flat.shape[0]
+        if x_flat.dtype != torch.float32 and (M <= MAX_GEMV_ROWS or
+                                              x_flat.dtype != torch.bfloat16):
+            # up to 16 rows, any float type is read as fp32 against the exact
+            # fp32 codebook values, as the reference's batch-1 kernels compute
+            # (.to(tl.float32), triton_kernel.py:46, 174-183)
+            x_flat = x_flat.to(torch.float32)
         N, K = self.out_features, self.in_features
         if M <= MAX_GEMV_ROWS:
             y = ops.gemv(x_flat, self.packed_indices, self.codebook, N, K, bits=self.bits,

@@ -361,8 +361,11 @@ def test_packed_linear_api(dev):
             x = torch.randn(*shape, generator=torch.Generator().manual_seed(len(shape))).to(xdt)
             y = layer(x.to(dev))
             assert y.dtype == torch.float32 and y.shape == (*shape[:-1], N)
-            # fp16 x is read as fp32 (the reference's kernels load x as fp32)
-            xr = x.float() if xdt == torch.float16 else x
+            # up to 16 rows every x is read as fp32 against the exact fp32
+            # codebook values (the reference's batch-1 kernels); more rows of
+            # bf16 x take the bf16 path, fp16 x is read as fp32
+            rows = x.numel() // K
+            xr = x if (xdt == torch.bfloat16 and rows > 16) else x.float()
             ref = ref_gemv(xr.reshape(-1, K), idx, cb, 128, N, K)
             assert rel(y.cpu().reshape(-1, N), ref) <= REL_F32
 
@@ -389,6 +392,15 @@ def test_kernels_mirror(dev):
     for fn in (kernels.dequant_matvec_3bit, kernels.dequant_matvec_3bit_cuda):
         y = fn(x.to(dev), pt, ct, N, K)
         assert y.shape == (N,) and rel(y.cpu(), ref) <= REL_F32
+    # bf16 x: the reference's runtime arithmetic (x read as fp32, exact fp32
+    # codebook values) -- within 1e-3 of the CUDA kernel's own fp32 order
+    xb = x.to(torch.bfloat16)
+    k1 = O.matvec_3bit_k1(xb.float().numpy(), p, cb, N, K)
+    refb = O.matmul_f64(xb.float().numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
+    for fn in (kernels.dequant_matvec_3bit, kernels.dequant_matvec_3bit_cuda):
+        yb = fn(xb.to(dev), pt, ct, N, K)
+        assert yb.dtype == torch.float32
+        assert rel(yb.cpu(), k1) <= 1e-3 and rel(yb.cpu(), refb) <= REL_F32
     # fp16 x is read as fp32, as the reference's Triton kernels do
     x16 = x.to(torch.float16)
     ref16 = O.matmul_f64(x16.float().numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))[0]
