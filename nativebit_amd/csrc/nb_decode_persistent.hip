@@ -629,6 +629,18 @@ void decode_persistent_kernel(PArgs args) {
     const int GP = args.n_steps * 4 * L;  // GEMV phases of the whole sequence
     int pos = ld_g(&args.st->pos), tok = ld_g(&args.st->token), step = ld_g(&args.st->step);
     unsigned nbar = 0;  // grid barriers passed (control wave)
+    // A token outside the embedding table never forms an address: it sets
+    // bit 1 of the error word (every workgroup then leaves at its next grid
+    // barrier, the launch ends normally) and row 0 is read instead.
+    auto checked_token = [&](int t) -> int {
+        if ((unsigned)t < (unsigned)args.V) return t;
+        if (tid == 0) {
+            __hip_atomic_fetch_or(as_global_mut(args.ctl + kCtlErr), 2u, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return 0;
+    };
+    tok = checked_token(tok);
 
     // ---- set-up: geometry of the four GEMV kinds for this workgroup, lane
     // table, the stream and codebook pointers of every layer and kind, and
@@ -891,7 +903,7 @@ void decode_persistent_kernel(PArgs args) {
         if (g == 0 && tid == 0 && step >= 0 && step < A->tokens_cap) {
             *as_global_mut(A->tokens_out + step) = am;
         }
-        tok = (step >= 0 && step < A->n_force) ? ld_g(A->force + step) : am;
+        tok = checked_token((step >= 0 && step < A->n_force) ? ld_g(A->force + step) : am);
         pos += 1;
         step += 1;
     }

@@ -247,3 +247,56 @@ def test_workgroup_count_fits_every_kind(kind):
     # the launcher's grid: one workgroup per CU, fewer when a kind has fewer
     # chunks; at the 2.2B shape every kind has at least 256 chunks
     assert geo(kind, 0)["nch"] >= G
+
+
+# -- the argmax key hand-over and the embedding address it drives ------------
+#
+# After the head phase every workgroup reads st->key, forms the chosen token
+# am = 0xffffffff - low32(key) and, at the next token's layer 0, reads the
+# embedding row emb_f32 + tok * C.  A key that holds no maximum (cleared, or
+# read before the max) gives am = 0xffffffff, i.e. token -1 as an int: the
+# row 10 KB before the table.  The kernel's checked_token maps any token
+# outside [0, V) to row 0 and sets bit 1 of the error word, so the address
+# stays inside the table and the launch ends at its next grid barrier.
+
+def _key(logit, row):
+    """The head's 64-bit key: order-preserving logit bits << 32 | ~row."""
+    import struct
+    b = struct.unpack("<I", struct.pack("<f", logit))[0]
+    ob = (b ^ 0xFFFFFFFF) if b & 0x80000000 else (b | 0x80000000)
+    return (ob << 32) | (0xFFFFFFFF - row)
+
+
+def _am(key):
+    v = 0xFFFFFFFF - (key & 0xFFFFFFFF)
+    return v - (1 << 32) if v & 0x80000000 else v   # the kernel's (int) cast
+
+
+def _checked(t, err):
+    if 0 <= t < V:
+        return t, err
+    return 0, err | 2
+
+
+def test_key_handover_model_and_token_guard():
+    src = open(SRC).read()
+    # the expressions modelled here are the kernel's
+    assert "(int)(0xffffffffu - (uint32_t)(key & 0xffffffffull))" in src
+    assert "if ((unsigned)t < (unsigned)args.V) return t;" in src
+    assert "tok = checked_token(" in src and "tok = checked_token(tok);" in src
+    emb_bytes = V * C * 4
+    # a merged key: the first row with the largest logit, in range
+    keys = [_key(1.5, 7), _key(3.25, 31999), _key(3.25, 40), _key(-2.0, 0)]
+    best = max(keys)
+    assert _am(best) == 40
+    # a key with no maximum in it: token -1, an address before the table
+    assert _am(0) == -1
+    assert -1 * C * 4 < 0
+    tok, err = _checked(_am(0), 0)
+    assert (tok, err) == (0, 2) and 0 <= tok * C * 4 and tok * C * 4 + C * 4 <= emb_bytes
+    # every valid token passes unchanged; every other int is caught
+    for t in (0, 1, V - 1):
+        assert _checked(t, 0) == (t, 0)
+    for t in (-1, V, V + 5, -(1 << 31), (1 << 31) - 1):
+        tt, e = _checked(t, 0)
+        assert tt == 0 and e == 2
