@@ -508,7 +508,9 @@ def bench_prefill(dev, random_weights=False):
         xs = {K: synth.make_activation(K, m=M, seed=M + K, device=dev, dtype=torch.bfloat16)
               for K in (2560, 6912)}
         per, tot_ms, tot_fl, ref_ms, blas_ms = {}, 0.0, 0, 0.0, 0.0
+        f32_ms, f32_ref_ms = 0.0, 0.0
         wx = {}
+        xf = {K: v.float() for K, v in xs.items()}
         for n, N, K in PREFILL_SHAPES:
             lay = layers[n]
             y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
@@ -519,35 +521,52 @@ def bench_prefill(dev, random_weights=False):
                 ops.dequant(lay.packed, lay.codebook, N * K, 3, 128, torch.bfloat16, out=wb)
                 torch.matmul(xs[K], wb.view(N, K).T, out=y)
 
+            yf = torch.empty(M, N, dtype=torch.float32, device=dev)
+            wf = torch.empty(N * K, dtype=torch.float32, device=dev)
+
+            def f32_ref(lay=lay, N=N, K=K, wb=wf):
+                # fp32 x the reference's way: W gathered at fp32, dense fp32 matmul
+                ops.dequant(lay.packed, lay.codebook, N * K, 3, 128, torch.float32, out=wb)
+                torch.matmul(xf[K], wb.view(N, K).T, out=yf)
+
             fns = [lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y),
                    lambda: ops.gemm_prefill(xs[K], lay.packed, lay.codebook, N, K, out=y,
                                             path="fused"),
                    expanded,
-                   lambda: torch.matmul(xs[K], w.T)]
+                   lambda: torch.matmul(xs[K], w.T),
+                   lambda: ops.gemm_prefill_f32(xf[K], lay.packed, lay.codebook, N, K, out=yf),
+                   f32_ref]
             # each form timed twice, in alternation, and the lower time kept
             # (the first graph timed after a shape change can run up to ~30 %
             # slow while the clocks settle)
             t = [min(a, b) for a, b in zip([graph_calls_time(f) for f in fns],
                                            [graph_calls_time(f) for f in fns])]
-            ms, ms_one, ms_blas, ms_ref = t
+            ms, ms_one, ms_blas, ms_ref, ms_f32, ms_f32_ref = t
             fl = 2 * M * N * K
             ws = int(_lib.load().nb_gemm_prefill_split_ws_bytes(M, N, K))
             per[n] = {"us": round(ms * 1e3, 1), "TFLOP_s": round(fl / ms / 1e9, 1),
                       "k_split_partials_MiB": round(ws / 2**20, 2),
                       "one_launch_us": round(ms_one * 1e3, 1),
                       "expand_then_torch_bf16_us": round(ms_blas * 1e3, 1),
-                      "torch_dense_bf16_us": round(ms_ref * 1e3, 1)}
+                      "torch_dense_bf16_us": round(ms_ref * 1e3, 1),
+                      "f32_x_us": round(ms_f32 * 1e3, 1),
+                      "f32_x_gather_then_torch_f32_us": round(ms_f32_ref * 1e3, 1)}
             tot_ms += ms
             blas_ms += ms_blas
             ref_ms += ms_ref
             tot_fl += fl
-            del w, wx[n]
+            f32_ms += ms_f32
+            f32_ref_ms += ms_f32_ref
+            del w, wx[n], wf
         out[f"M{M}"] = {"layer_us": round(tot_ms * 1e3, 1),
                         "TFLOP_s": round(tot_fl / tot_ms / 1e9, 1),
                         "pct_bf16_mfma_peak": round(tot_fl / tot_ms / 1e9 / 2500 * 100, 2),
                         "model_26_layers_ms": round(26 * tot_ms, 3),
                         "expand_then_torch_bf16_layer_us": round(blas_ms * 1e3, 1),
                         "torch_dense_bf16_layer_us": round(ref_ms * 1e3, 1),
+                        "f32_x_layer_us": round(f32_ms * 1e3, 1),
+                        "f32_x_TFLOP_s": round(tot_fl / f32_ms / 1e9, 1),
+                        "f32_x_gather_then_torch_f32_layer_us": round(f32_ref_ms * 1e3, 1),
                         "per_matmul": per}
     out["note"] = ("us / TFLOP_s: nb_gemm_prefill_split, the hand-written MFMA kernels that "
                    "read the 3-bit stream and codebooks and dequantize into LDS (bf16 operands, "
@@ -561,7 +580,11 @@ def bench_prefill(dev, random_weights=False):
                    "(hipBLASLt), the expansion inside the timed call, "
                    "torch_dense_bf16 = torch.matmul on an already-unpacked bf16 weight (the "
                    "reference's path also unpacks and gathers W on every call, "
-                   "triton_kernel.py:258-275)")
+                   "triton_kernel.py:258-275); f32_x = nb_gemm_prefill_f32 for fp32 activations "
+                   "against the exact fp32 weights (three bf16 MFMA passes over the hi / lo parts "
+                   "of x and W, fp32-level products), beside f32_x_gather_then_torch_f32 = the "
+                   "reference's fp32 batched branch on the GPU (nb_dequant to fp32 W, then "
+                   "torch.matmul in fp32)")
     return out
 
 

@@ -131,6 +131,28 @@ int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* packed,
                           int K, void* workspace, int64_t ws_bytes, void* stream);
 
 /*
+ * The same contraction for fp32 activations against the exact fp32 codebook
+ * values, y[m][n] = sum_k x[m][k] * W[n][k] (x fp32 row stride ldx, y fp32
+ * row stride ldy, any alignment of their element type; K % 128 == 0), on
+ * the bf16 MFMA kernel in three passes: x = hi + lo and W = W_hi + W_lo
+ * split into bf16 parts (hi = bf16(v), lo = bf16(v - hi); W_lo through the
+ * residual codebook cb - bf16(cb) over the same indices), y = hi.W_hi +
+ * hi.W_lo + lo.W_hi accumulated in fp32 in that order.  Each product is x.W
+ * to within 2^-16 of its size (the dropped lo.W_lo and the bf16 roundings
+ * of the lo parts), against 2^-24 for an fp32 product; W is never
+ * materialised.  The workspace needs nb_gemm_prefill_f32_ws_bytes(M, N, K)
+ * bytes, 256-byte aligned (the bf16 parts of x, the residual codebook, the
+ * K-split partial products), contents clobbered.  Deterministic.
+ * Replaces: the batched branch of PackedLinear.forward for fp32 x
+ *           (unpack + gather + x @ W.T, inference/triton_kernel.py:258-275;
+ *           nativebit/inference.py:42-46), without the per-call W.
+ */
+int64_t nb_gemm_prefill_f32_ws_bytes(int M, int N, int K);
+int nb_gemm_prefill_f32(const float* x, int64_t ldx, const uint8_t* packed,
+                        const float* codebook, float* y, int64_t ldy, int M, int N, int K,
+                        void* workspace, int64_t ws_bytes, void* stream);
+
+/*
  * Unpack `count` indices of `bits` bits to one byte each.
  * Replaces: unpack_3bit / unpack_4bit / unpack_nbits
  *           (nativebit/pack.py:44-68, 85-90, 119-138) and

@@ -68,6 +68,8 @@ SIGNATURES = {
     "nb_gemm_prefill": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P]),
     "nb_gemm_prefill_split_ws_bytes": (_L, [_I, _I, _I]),
     "nb_gemm_prefill_split": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P, _L, _P]),
+    "nb_gemm_prefill_f32_ws_bytes": (_L, [_I, _I, _I]),
+    "nb_gemm_prefill_f32": (_I, [_P, _L, _P, _P, _P, _L, _I, _I, _I, _P, _L, _P]),
     "nb_add_rmsnorm": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, ctypes.c_float, _P]),
     "nb_attention_step": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "nb_attention_work_floats": (_I, [_I]),

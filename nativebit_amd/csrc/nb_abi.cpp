@@ -809,6 +809,38 @@ extern "C" int nb_gemm_prefill_split(const void* x, int64_t ldx, const uint8_t* 
                            static_cast<hipStream_t>(stream));
 }
 
+extern "C" int64_t nb_gemm_prefill_f32_ws_bytes(int M, int N, int K) {
+    return prefill_f32_bytes(M, N, K);
+}
+
+extern "C" int nb_gemm_prefill_f32(const float* x, int64_t ldx, const uint8_t* packed,
+                                   const float* codebook, float* y, int64_t ldy, int M, int N,
+                                   int K, void* workspace, int64_t ws_bytes, void* stream) {
+    const char* fn = "nb_gemm_prefill_f32";
+    if (M < 0 || N < 0 || K < 0) return fail(NB_EINVAL, "%s: negative shape", fn);
+    if (K % 128 != 0) return fail(NB_EUNSUPPORTED, "%s: K=%d not a multiple of 128", fn, K);
+    if ((int64_t)N * (K / 128) >= (1LL << 31) || (int64_t)M * K >= (1LL << 40)) {
+        return fail(NB_EUNSUPPORTED, "%s: shape too large", fn);
+    }
+    if (M == 0 || N == 0) return NB_OK;
+    if (K == 0) return fail(NB_EUNSUPPORTED, "%s: K == 0 (use nb_gemv)", fn);
+    if (ldx < K || ldy < N) return fail(NB_EINVAL, "%s: ldx=%lld < K or ldy=%lld < N", fn,
+                                        (long long)ldx, (long long)ldy);
+    if (!x || !packed || !codebook || !y || !workspace) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(x, 4) || !aligned(y, 4)) return fail(NB_EALIGN, "%s: x or y not 4-byte aligned", fn);
+    if (!aligned(packed, 8) || !aligned(codebook, 16)) return fail(NB_EALIGN, "%s: packed 8- / codebook 16-byte alignment", fn);
+    if (!aligned(workspace, 256)) return fail(NB_EALIGN, "%s: workspace not 256-byte aligned", fn);
+    const int dev_st = ensure_device();
+    const int64_t need = prefill_f32_bytes(M, N, K);
+    if (ws_bytes < need) {
+        return fail(NB_EINVAL, "%s: workspace of %lld bytes < %lld", fn, (long long)ws_bytes,
+                    (long long)need);
+    }
+    if (dev_st) return dev_st;
+    return launch_prefill_f32(x, ldx, packed, codebook, y, ldy, M, N, K, workspace, ws_bytes,
+                              static_cast<hipStream_t>(stream));
+}
+
 namespace {
 // Shapes and pointers of a persistent-decode model; NB_OK or a status.
 int check_decode_model(const nb_decode_model* m, const char* fn) {

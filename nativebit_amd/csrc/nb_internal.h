@@ -134,8 +134,15 @@ int launch_dequant(const uint8_t* packed, const float* codebook, void* w,
 // launch over all of K.
 int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
                     void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
-                    int64_t ws_bytes, hipStream_t stream);
+                    int64_t ws_bytes, hipStream_t stream, bool accumulate = false);
 int64_t prefill_split_bytes(int M, int N, int K);
+// fp32 activations: x split into bf16 hi + lo, the residual codebook cb -
+// bf16(cb), three prefill passes accumulated in fp32 (workspace of
+// prefill_f32_bytes(M, N, K) bytes, 256-byte aligned).
+int64_t prefill_f32_bytes(int M, int N, int K);
+int launch_prefill_f32(const float* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                       float* y, int64_t ldy, int M, int N, int K, void* workspace,
+                       int64_t ws_bytes, hipStream_t stream);
 
 // Decode-step kernels (nb_decode.hip).
 int launch_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* st,

@@ -107,6 +107,7 @@ struct Prefill2Args {
     int M, N, K;
     int ksplit;   // K ranges per output tile (1: the whole of K)
     float* part;  // ksplit > 1: fp32 partial products [ksplit][M][N], else null
+    int accumulate;  // fp32 y only: y += result instead of y = result
 };
 
 // One thread's share of a W slice: 12 index bytes (32 weights) per half
@@ -318,12 +319,14 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
                 }
             } else {
                 float* yp = static_cast<float*>(yb) + (int64_t)m * ldy + n;
+                const bool acc_y = !partial && a.accumulate;
                 if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-                    *reinterpret_cast<f32x4_t*>(yp) = v;
+                    *reinterpret_cast<f32x4_t*>(yp) =
+                        acc_y ? *reinterpret_cast<const f32x4_t*>(yp) + v : v;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        if (n + e < a.N) yp[e] = v[e];
+                        if (n + e < a.N) yp[e] = acc_y ? yp[e] + v[e] : v[e];
                 }
             }
         }
@@ -332,11 +335,12 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
 
 // y[m][n] = sum over k ranges s = 0, 1, ... of part[s][m][n] (in that
 // order, so the result does not depend on which workgroup finished first),
-// converted to y's dtype.  Four consecutive outputs per thread where the
-// rows allow it.
+// converted to y's dtype (added to fp32 y with accumulate).  Four
+// consecutive outputs per thread where the rows allow it.
 __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __restrict__ part,
                                                              int S, int M, int N, void* y,
-                                                             int y_dtype, int64_t ldy) {
+                                                             int y_dtype, int64_t ldy,
+                                                             int accumulate) {
     const int64_t plane = (int64_t)M * N;
     // four outputs a thread where every row starts on a 4-output boundary
     // of both part and y (rows of 4k outputs, bases aligned for the vector
@@ -357,7 +361,8 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
                 p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
                 *reinterpret_cast<u32x2_t*>(static_cast<bf16_bits*>(y) + m * ldy + n) = p;
             } else {
-                *reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + m * ldy + n) = v;
+                f32x4_t* yp = reinterpret_cast<f32x4_t*>(static_cast<float*>(y) + m * ldy + n);
+                *yp = accumulate ? *yp + v : v;
             }
         } else {
             const int64_t m = i / N, n = i - m * N;
@@ -366,7 +371,8 @@ __global__ __launch_bounds__(256) void prefill_reduce_kernel(const float* __rest
             if (y_dtype == NB_BF16) {
                 static_cast<bf16_bits*>(y)[m * ldy + n] = f32_to_bf16_rne(v);
             } else {
-                static_cast<float*>(y)[m * ldy + n] = v;
+                float* yp = static_cast<float*>(y) + m * ldy + n;
+                *yp = accumulate ? *yp + v : v;
             }
         }
     }
@@ -415,7 +421,72 @@ PrefillPlan prefill_plan(int M, int N, int K, bool allow_split) {
     return {64, 128, 1};
 }
 
+// x (M rows, stride ldx, fp32) -> hi = bf16(x), lo = bf16(x - hi), rows of
+// K (contiguous).  x - hi is exact in fp32, so hi + lo is x to 2^-18.
+__global__ __launch_bounds__(256) void split_bf16_kernel(const float* __restrict__ x, int64_t ldx,
+                                                         bf16_bits* __restrict__ hi,
+                                                         bf16_bits* __restrict__ lo, int M, int K) {
+    const int64_t total = (int64_t)M * K;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 256) {
+        const int64_t m = i / K, k = i - m * K;
+        const float v = x[m * ldx + k];
+        const bf16_bits h = f32_to_bf16_rne(v);
+        hi[i] = h;
+        lo[i] = f32_to_bf16_rne(v - bf16_to_f32(h));
+    }
+}
+
+// The residual codebook: cb_lo = cb - bf16(cb) (exact in fp32).
+__global__ __launch_bounds__(256) void cb_residual_kernel(const float* __restrict__ cb,
+                                                          float* __restrict__ cb_lo, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * 256) {
+        const float v = cb[i];
+        cb_lo[i] = v - bf16_to_f32(f32_to_bf16_rne(v));
+    }
+}
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
 }  // namespace
+
+int64_t prefill_f32_bytes(int M, int N, int K) {
+    if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
+    const int64_t xb = align256((int64_t)M * K * 2);
+    const int64_t cb = align256((int64_t)N * (K / 128) * 8 * 4);
+    return 2 * xb + cb + prefill_split_bytes(M, N, K);
+}
+
+int launch_prefill_f32(const float* x, int64_t ldx, const uint8_t* packed, const float* codebook,
+                       float* y, int64_t ldy, int M, int N, int K, void* workspace,
+                       int64_t ws_bytes, hipStream_t stream) {
+    unsigned char* w = static_cast<unsigned char*>(workspace);
+    const int64_t xb = align256((int64_t)M * K * 2);
+    const int64_t nent = (int64_t)N * (K / 128) * 8;
+    bf16_bits* hi = reinterpret_cast<bf16_bits*>(w);
+    bf16_bits* lo = reinterpret_cast<bf16_bits*>(w + xb);
+    float* cb_lo = reinterpret_cast<float*>(w + 2 * xb);
+    unsigned char* split = w + 2 * xb + align256(nent * 4);
+    const int64_t split_bytes = ws_bytes - (split - w);
+    const unsigned g1 = (unsigned)std::min<int64_t>(((int64_t)M * K + 255) / 256, 8192);
+    hipLaunchKernelGGL(split_bf16_kernel, dim3(g1), dim3(256), 0, stream, x, ldx, hi, lo, M, K);
+    const unsigned g2 = (unsigned)std::min<int64_t>((nent + 255) / 256, 4096);
+    hipLaunchKernelGGL(cb_residual_kernel, dim3(g2), dim3(256), 0, stream, codebook, cb_lo, nent);
+    int st = check_launch("nb_gemm_prefill_f32");
+    if (st) return st;
+    void* sw = split_bytes > 0 ? static_cast<void*>(split) : nullptr;
+    // x.W ~= hi.bf16(cb) + hi.bf16(cb_lo) + lo.bf16(cb), each pass in fp32,
+    // added to y in that order
+    st = launch_prefill2(hi, K, packed, codebook, y, NB_F32, ldy, M, N, K, sw, split_bytes, stream,
+                         false);
+    if (st) return st;
+    st = launch_prefill2(hi, K, packed, cb_lo, y, NB_F32, ldy, M, N, K, sw, split_bytes, stream,
+                         true);
+    if (st) return st;
+    return launch_prefill2(lo, K, packed, codebook, y, NB_F32, ldy, M, N, K, sw, split_bytes,
+                           stream, true);
+}
 
 int64_t prefill_split_bytes(int M, int N, int K) {
     if (M <= 0 || N <= 0 || K <= 0 || K % 128) return 0;
@@ -425,8 +496,9 @@ int64_t prefill_split_bytes(int M, int N, int K) {
 
 int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const float* codebook,
                     void* y, int y_dtype, int64_t ldy, int M, int N, int K, void* workspace,
-                    int64_t ws_bytes, hipStream_t stream) {
+                    int64_t ws_bytes, hipStream_t stream, bool accumulate) {
     Prefill2Args a;
+    a.accumulate = accumulate ? 1 : 0;
     a.x = static_cast<const uint16_t*>(x);
     a.ldx = ldx;
     a.packed = packed;
@@ -462,7 +534,7 @@ int launch_prefill2(const void* x, int64_t ldx, const uint8_t* packed, const flo
         const int64_t items = ((N | ldy) & 3) == 0 ? (int64_t)M * N / 4 : (int64_t)M * N;
         const unsigned rg = (unsigned)std::min<int64_t>((items + 255) / 256, 4096);
         hipLaunchKernelGGL(prefill_reduce_kernel, dim3(rg), dim3(256), 0, stream, a.part, p.S,
-                           M, N, y, y_dtype, ldy);
+                           M, N, y, y_dtype, ldy, a.accumulate);
     }
     return check_launch("nb_gemm_prefill");
 }

@@ -11,10 +11,11 @@ default.  Differences, all deliberate:
   the exact fp32 codebook values (the reference's batch-1 arithmetic, for
   bf16 and fp16 x too); more rows of bf16 activations run the packed MFMA
   prefill kernels (bf16-rounded codebook values, the reference's bf16 path
-  of eval_ppl.py:149-174 -- its fp32 batched branch rejects bf16 x), and
-  other batched inputs (fp32 x, other formats) gather W on the device with
-  the format kernel and multiply it densely, as the reference's batched
-  branch does; nothing falls back silently -- a failure raises
+  of eval_ppl.py:149-174 -- its fp32 batched branch rejects bf16 x); more
+  rows of fp32 x run the same MFMA kernels in three bf16 passes over the hi
+  and lo parts of x and W (fp32-level products); other formats gather W on
+  the device with the format kernel and multiply it densely, as the
+  reference's batched branch does; nothing falls back silently -- a failure raises
   NativeBitError (the reference swallows every exception,
   triton_kernel.py:252);
 * bit width, entries per block and block size are attributes (defaults 3, 8
@@ -87,6 +88,12 @@ class PackedLinear(torch.nn.Module):
             # the bf16 batched form (eval_ppl.py:149-174): the packed MFMA kernels
             y = ops.gemm_prefill(x_flat, self.packed_indices, self.codebook, N, K,
                                  out_dtype=self.out_dtype)
+        elif self._standard():
+            # the reference's fp32 batched branch (triton_kernel.py:258-275) on
+            # the packed MFMA kernels: three bf16 passes over the hi / lo parts
+            # of x and of the exact fp32 weights, W never materialised
+            y = ops.gemm_prefill_f32(x_flat.contiguous(), self.packed_indices, self.codebook,
+                                     N, K).to(self.out_dtype)
         else:
             # the reference's batched branch as it computes it (triton_kernel.py:
             # 258-275): W gathered on the device at x's precision by the format

@@ -335,6 +335,37 @@ def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, 
     return out
 
 
+
+def gemm_prefill_f32(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
+                     K: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = x @ W.T for fp32 x (M, K) against the exact fp32 codebook values of
+    a 3-bit / 8-entry / block-128 packed W (N x K), y fp32 (M, N):
+    nb_gemm_prefill_f32, three bf16 MFMA passes over the hi / lo parts of x
+    and W (each product to within 2^-16 of its size), the packed weight
+    dequantized into LDS tiles, never materialised; a workspace from torch's
+    allocator."""
+    for name, t in (("x", x), ("packed", packed), ("codebook", codebook)):
+        _require_cuda(name, t)
+    _same_device(x, packed, codebook)
+    if x.dim() != 2 or x.shape[1] != K or x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError(f"x must be a row-contiguous (M, {K}) float32 tensor")
+    if codebook.shape != (N * K // 128, 8) or codebook.dtype != torch.float32:
+        raise ValueError("codebook must be (N*K/128, 8) float32")
+    if packed.dtype != torch.uint8 or packed.numel() < packed_nbytes(N * K, 3):
+        raise ValueError("packed must hold the 3-bit stream of N*K indices")
+    M = x.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=x.device)
+    elif out.shape != (M, N) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError("out must be (M, N) float32, row-contiguous")
+    lib = _lib.load()
+    nbytes = int(lib.nb_gemm_prefill_f32_ws_bytes(M, N, K))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.check(lib.nb_gemm_prefill_f32(
+        x.data_ptr(), x.stride(0), packed.data_ptr(), codebook.data_ptr(), out.data_ptr(),
+        out.stride(0), M, N, K, ws.data_ptr(), nbytes, _stream(x)))
+    return out
+
 def unpack(packed: torch.Tensor, count: int, bits: int) -> torch.Tensor:
     """uint8 indices from an LSB-first stream (device)."""
     _require_cuda("packed", packed)

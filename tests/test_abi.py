@@ -535,3 +535,43 @@ def test_rmsnorm_rows_validation(kw, status):
 def test_rmsnorm_rows_vocab_ignored_without_lookup():
     assert _lib.load().nb_rmsnorm_rows(FAKE, None, None, None, 0, FAKE, FAKE, _lib.NB_F32, 0,
                                        256, 1e-6, None) == _lib.NB_OK
+
+
+def test_prefill_f32_ws_bytes():
+    lib = _lib.load()
+    # bf16 hi and lo parts of x (256-byte rounded), the residual codebook,
+    # the split partials of the bf16 kernel
+    for M, N, K in ((17, 128, 128), (2048, 2560, 2560), (128, 2560, 6912)):
+        xb = -(-M * K * 2 // 256) * 256
+        cb = -(-N * (K // 128) * 8 * 4 // 256) * 256
+        split = int(lib.nb_gemm_prefill_split_ws_bytes(M, N, K))
+        assert lib.nb_gemm_prefill_f32_ws_bytes(M, N, K) == 2 * xb + cb + split
+    assert lib.nb_gemm_prefill_f32_ws_bytes(4, 4, 100) == 0
+
+
+def prefill_f32(**kw):
+    lib = _lib.load()
+    a = dict(x=FAKE, ldx=256, packed=FAKE, codebook=FAKE, y=FAKE, ldy=64, M=32, N=64, K=256,
+             ws=FAKE, ws_bytes=int(lib.nb_gemm_prefill_f32_ws_bytes(32, 64, 256)), stream=None)
+    a.update(kw)
+    return lib.nb_gemm_prefill_f32(*a.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(K=200), _lib.NB_EUNSUPPORTED),
+    (dict(M=-1), _lib.NB_EINVAL),
+    (dict(ldx=128), _lib.NB_EINVAL),
+    (dict(ldy=10), _lib.NB_EINVAL),
+    (dict(ws=None), _lib.NB_EINVAL),
+    (dict(ws=FAKE + 16), _lib.NB_EALIGN),
+    (dict(ws_bytes=1024), _lib.NB_EINVAL),
+    (dict(x=FAKE + 2), _lib.NB_EALIGN),
+    (dict(codebook=FAKE + 4), _lib.NB_EALIGN),
+])
+def test_prefill_f32_validation(kw, status):
+    assert prefill_f32(**kw) == status
+    assert _lib.last_error().startswith("nb_gemm_prefill_f32")
+
+
+def test_prefill_f32_empty_is_ok():
+    assert prefill_f32(M=0) == _lib.NB_OK and prefill_f32(N=0) == _lib.NB_OK

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from nativebit_amd import ops, synth
+from nativebit_amd import _lib, ops, synth
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -216,3 +216,64 @@ def test_prefill_m2048_2p2b(dev, name, path, ydt):
     got = y.float().cpu().numpy()[rows]
     assert np.isfinite(got).all()
     assert rel(got, ref) <= (1e-3 if ydt == torch.float32 else 1e-2), rel(got, ref)
+
+
+# fp32 activations against the exact fp32 codebook values (nb_gemm_prefill_f32:
+# three bf16 passes over the hi / lo parts of x and W).  Each product is x.W to
+# within 2^-16 of its size, so the sums stay within 1e-5 of the fp64 brute
+# force on the exact weights (the north star's fp32 bar is 1e-3).
+F32_CASES = [(17, 128, 128), (40, 300, 384), (200, 2560, 2560), (512, 7680, 2560),
+             (128, 2560, 6912), (100, 1998, 6912), (2048, 2560, 2560)]
+
+
+@pytest.mark.parametrize("M,N,K", F32_CASES)
+def test_prefill_f32_vs_f64(dev, M, N, K):
+    note(f"prefill f32 M={M} N={N} K={K}")
+    idx, p, cb = layer(N, K, M + 3 * N)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(M * 5 + K))
+    pd, cd = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    y = ops.gemm_prefill_f32(x.to(dev), pd, cd, N, K)
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)        # exact fp32 weights
+    rows = np.arange(M) if M * N * K <= 2e8 else np.unique(np.linspace(0, M - 1, 24).astype(int))
+    ref = O.matmul_f64(x.numpy()[rows], w)
+    got = y.cpu().numpy()[rows]
+    assert np.isfinite(got).all()
+    assert rel(got, ref) <= 1e-5, rel(got, ref)
+    # the bf16 path on the same x differs by the bf16 roundings (~1e-3): the
+    # fp32 path is the more exact one
+    yb = ops.gemm_prefill(x.to(torch.bfloat16).to(dev), pd, cd, N, K, out_dtype=torch.float32)
+    assert rel(yb.cpu().numpy()[rows], ref) > 10 * rel(got, ref)
+
+
+def test_prefill_f32_strided_and_deterministic(dev):
+    M, N, K = 96, 260, 640
+    idx, p, cb = layer(N, K, 77)
+    pd, cd = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+    big = torch.randn(M, K + 3, generator=torch.Generator().manual_seed(8)).to(dev)
+    x = big[:, 1:K + 1]                                      # odd offset, row stride K + 3
+    out = torch.full((M, N + 5), float("nan"), device=dev)[:, 2:N + 2]
+    lib = _lib.load()
+    nbytes = int(lib.nb_gemm_prefill_f32_ws_bytes(M, N, K))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    s = torch.cuda.current_stream().cuda_stream
+    for _ in range(2):
+        _lib.check(lib.nb_gemm_prefill_f32(x.data_ptr(), x.stride(0), pd.data_ptr(), cd.data_ptr(),
+                                           out.data_ptr(), out.stride(0), M, N, K, ws.data_ptr(),
+                                           nbytes, s))
+        first = out.clone() if _ == 0 else first
+    assert torch.equal(out, first)
+    w = O.dequant(idx, cb, 128, N * K).reshape(N, K)
+    ref = O.matmul_f64(x.cpu().numpy(), w)
+    assert rel(out.cpu().numpy(), ref) <= 1e-5
+
+
+def test_packed_linear_f32_batched_uses_exact_weights(dev):
+    """PackedLinear with fp32 x and more than 16 rows: the fp32 MFMA path."""
+    from nativebit_amd import PackedLinear
+    N, K, M = 640, 2560, 300
+    idx, p, cb = layer(N, K, 5)
+    lin = PackedLinear(torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev), N, K)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(6))
+    y = lin(x.to(dev))
+    ref = O.matmul_f64(x.numpy(), O.dequant(idx, cb, 128, N * K).reshape(N, K))
+    assert y.dtype == torch.float32 and rel(y.cpu().numpy(), ref) <= 1e-5
