@@ -594,13 +594,16 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
     batched: one launch per step -- nb_gemv_batched (the streaming kernel)
     at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2..4
     (the layers re-ordered once by nb_quad_layout, outside the timing, as
-    at model load), nb_gemm_skinny_batched at M > 4 -- replayed as a HIP
-    graph; rows_layout: nb_gemm_skinny_batched on the original layout, for
+    at model load), nb_gemm_skinny_tile_batched on the tile layout at M > 4
+    (nb_tile_layout, likewise once) -- replayed as a HIP graph;
+    rows_layout: nb_gemm_skinny_batched on the original layout, for
     comparison; per_matmul: 182 nb_gemv launches per step (one per matmul)
     in a graph."""
     from nativebit_amd import ops, synth
     mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
-    quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats]
+    quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats] \
+        if any(2 <= M <= 4 for M in ms) else []
+    tiles = [ops.tile_layout(m.packed, m.cb, m.N, m.K) for m in mats] if max(ms) > 4 else []
     torch.cuda.synchronize()
     out = {}
     for M in ms:
@@ -627,6 +630,18 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
             extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
                      "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
             del yq, qbatch
+        elif M > 4:
+            yq = [torch.empty(M, m.N, device=dev) for m in mats]
+            sbatch = ops.GemvBatch([(xs[m.K], t[0], t[1], y, m.N, m.K)
+                                    for m, t, y in zip(mats, tiles, yq)], m=M, layout="tile")
+            ms_b = graph_time(sbatch.run, 20, 5)
+            kernel = "gemv_skinny_kernel (tile layout)"
+            # the same MFMAs in the same order: the same bits
+            if not all(torch.equal(a, b) for a, b in zip(yq, ys)):
+                raise RuntimeError(f"skinny M={M}: tile and row layouts disagree")
+            extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
+                     "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
+            del yq, sbatch
 
         def run():
             for m, y in zip(mats, ys):
@@ -641,10 +656,11 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
             f"{kernel}), per-matmul launches {ms_p*1e3:.1f} us")
         del ys, xs, batch
     out["note"] = ("batched: every matmul of the step in one launch (graph replay); M = 2..4 "
-                   "on the row-quad layout (nb_quad_layout, once, untimed), rows_layout the "
-                   "same products on the original layout; per_matmul: 182 nb_gemv launches "
-                   "per step in one graph")
-    del quads
+                   "on the row-quad layout (nb_quad_layout, once, untimed), M > 4 on the "
+                   "tile layout (nb_tile_layout, once, untimed; bit-identical to the "
+                   "original layout's products), rows_layout the same products on the "
+                   "original layout; per_matmul: 182 nb_gemv launches per step in one graph")
+    del quads, tiles
     return out
 
 

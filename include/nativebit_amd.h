@@ -316,6 +316,36 @@ int nb_quad_layout(const uint8_t* packed, const float* codebook, int N, int K,
 int nb_gemm_skinny_quad_batched(const nb_batch_item* items, const void* table_dev, int count,
                                 int M, int y_dtype, void* stream);
 
+/* Tile layout of a 3-bit / 8-entry / block-128 N x K layer for the skinny
+ * kernel: tiles of 16 rows x 4 column blocks (tile g * ceil(K/512) + s =
+ * rows 16g .. 16g + 15, column blocks 4s .. 4s + 3; rows past N and blocks
+ * past K/128 zero), each stored as 3072 index bytes in tpacked and 512
+ * fp32 codebook entries in tcodebook, in the order the kernel's LDS slot
+ * holds them: row r's 48-byte blocks b at block place
+ * (b + ((r >> 1) & 3) + (r >> 3)) & 3 of its 192 bytes, its codebook
+ * 16-byte pieces p at place (p + ((r & 6) | ((r ^ (r >> 3)) & 1))) & 7 of
+ * its 128 bytes, and within every 12-byte unit of 32 indices index 4s + t
+ * (s = 0..7, t = 0..3) at index position o(s) + 8t,
+ * o = (0, 1, 3, 4, 6, 7, 2, 5).  tpacked holds nb_tile_layout_bytes(N, K)
+ * bytes, tcodebook nb_tile_layout_bytes(N, K) * 2 / 3 bytes; all four
+ * pointers 16-byte aligned.
+ * No counterpart in the reference: a one-time re-ordering of a layer (for
+ * instance at model load) for nb_gemm_skinny_tile_batched. */
+int64_t nb_tile_layout_bytes(int N, int K);
+int nb_tile_layout(const uint8_t* packed, const float* codebook, int N, int K, uint8_t* tpacked,
+                   float* tcodebook, void* stream);
+
+/* nb_gemm_skinny_batched (M = 1..16) on layers in the tile layout: every
+ * item's packed / codebook are nb_tile_layout's output for that item's
+ * N x K; x, y, y_mode and table_dev as for nb_gemm_skinny_batched.  The
+ * same products, bit for bit, with each wave's slice read by five
+ * contiguous 1 KiB loads and less dequantization work per weight.
+ * Replaces the same reference branch (inference/triton_kernel.py:258-275,
+ * bf16 form of inference/eval_ppl.py:149-174) for the five to sixteen
+ * token rows of a small-batch decode step. */
+int nb_gemm_skinny_tile_batched(const nb_batch_item* items, const void* table_dev, int count,
+                                int M, int y_dtype, void* stream);
+
 
 /* ------------------------------------------------------------------------
  * Decode step (one token, batch 1) -- the non-GEMV kernels of the packed

@@ -65,6 +65,9 @@ SIGNATURES = {
     "nb_quad_layout_bytes": (_L, [_I, _I]),
     "nb_quad_layout": (_I, [_P, _P, _I, _I, _P, _P, _P]),
     "nb_gemm_skinny_quad_batched": (_I, [_P, _P, _I, _I, _I, _P]),
+    "nb_tile_layout_bytes": (_L, [_I, _I]),
+    "nb_tile_layout": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "nb_gemm_skinny_tile_batched": (_I, [_P, _P, _I, _I, _I, _P]),
     "nb_gemm_prefill": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P]),
     "nb_gemm_prefill_split_ws_bytes": (_L, [_I, _I, _I]),
     "nb_gemm_prefill_split": (_I, [_P, _L, _P, _P, _P, _I, _L, _I, _I, _I, _P, _L, _P]),

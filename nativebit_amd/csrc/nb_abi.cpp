@@ -436,11 +436,16 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
 
 namespace {
 
-// nb_gemm_skinny_batched and its row-quad form: shared validation, then
-// the kernel the layout calls for.
+enum SkinnyLayout { kLayoutRows, kLayoutQuad, kLayoutTile };
+
+// nb_gemm_skinny_batched and its row-quad and tile forms: shared
+// validation, then the kernel the layout calls for.
 int skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
-                   int y_dtype, void* stream, bool quad) {
-    const char* fn = quad ? "nb_gemm_skinny_quad_batched" : "nb_gemm_skinny_batched";
+                   int y_dtype, void* stream, SkinnyLayout layout) {
+    const bool quad = layout == kLayoutQuad;
+    const char* fn = quad                  ? "nb_gemm_skinny_quad_batched"
+                     : layout == kLayoutTile ? "nb_gemm_skinny_tile_batched"
+                                            : "nb_gemm_skinny_batched";
     int64_t chunks = 0;
     int mk = 0;
     int st = check_batch(items, count, fn, &chunks, &mk);
@@ -481,7 +486,7 @@ int skinny_batched(const nb_batch_item* items, const void* table_dev, int count,
                                 M, y_dtype, static_cast<hipStream_t>(stream));
     }
     return launch_gemv_skinny(static_cast<const StreamProblem*>(table_dev), host.data(), nprob, M,
-                              y_dtype, static_cast<hipStream_t>(stream));
+                              y_dtype, layout == kLayoutTile, static_cast<hipStream_t>(stream));
 }
 
 }  // namespace
@@ -490,12 +495,17 @@ extern "C" {
 
 int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, int count, int M,
                            int y_dtype, void* stream) {
-    return skinny_batched(items, table_dev, count, M, y_dtype, stream, false);
+    return skinny_batched(items, table_dev, count, M, y_dtype, stream, kLayoutRows);
 }
 
 int nb_gemm_skinny_quad_batched(const nb_batch_item* items, const void* table_dev, int count,
                                 int M, int y_dtype, void* stream) {
-    return skinny_batched(items, table_dev, count, M, y_dtype, stream, true);
+    return skinny_batched(items, table_dev, count, M, y_dtype, stream, kLayoutQuad);
+}
+
+int nb_gemm_skinny_tile_batched(const nb_batch_item* items, const void* table_dev, int count,
+                                int M, int y_dtype, void* stream) {
+    return skinny_batched(items, table_dev, count, M, y_dtype, stream, kLayoutTile);
 }
 
 int64_t nb_quad_layout_bytes(int N, int K) {
@@ -520,6 +530,31 @@ int nb_quad_layout(const uint8_t* packed, const float* codebook, int N, int K, u
     const int st = ensure_device();
     if (st) return st;
     return launch_quad_layout(packed, codebook, N, K, qpacked, qcodebook,
+                              static_cast<hipStream_t>(stream));
+}
+
+int64_t nb_tile_layout_bytes(int N, int K) {
+    if (N < 0 || K < 0 || K % 128) return 0;
+    return tile_layout_tiles(N, K) * 3072;
+}
+
+int nb_tile_layout(const uint8_t* packed, const float* codebook, int N, int K, uint8_t* tpacked,
+                   float* tcodebook, void* stream) {
+    const char* fn = "nb_tile_layout";
+    if (N < 0 || K <= 0 || K % 128) {
+        return fail(NB_EINVAL, "%s: N=%d K=%d (needs N >= 0, K > 0, K %% 128 == 0)", fn, N, K);
+    }
+    if (N == 0) return NB_OK;
+    if (!packed || !codebook || !tpacked || !tcodebook) {
+        return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    }
+    if (!aligned(packed, 16) || !aligned(codebook, 16) || !aligned(tpacked, 16) ||
+        !aligned(tcodebook, 16)) {
+        return fail(NB_EALIGN, "%s: packed/codebook/tpacked/tcodebook not 16-byte aligned", fn);
+    }
+    const int st = ensure_device();
+    if (st) return st;
+    return launch_tile_layout(packed, codebook, N, K, tpacked, tcodebook,
                               static_cast<hipStream_t>(stream));
 }
 

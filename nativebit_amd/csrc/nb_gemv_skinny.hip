@@ -18,9 +18,10 @@
 // global_load_lds_dwordx4: five instructions of 1 KiB, in which the lanes of
 // one row read that row's contiguous 192 (128) bytes, so every instruction
 // touches a few whole cache lines.  Within a row the 16-byte pieces land
-// rotated -- index blocks by (r >> 1) & 3 blocks, codebook pieces by r & 7
-// pieces -- which makes the compute side's LDS reads conflict-free.  Slices
-// i + 1 and i + 2 are in flight while slice i is computed.  The x slice
+// rotated -- index blocks by idx_rot(r) blocks, codebook pieces by
+// cb_rot(r) pieces -- which makes the compute side's LDS reads
+// conflict-free.  Slices i + 1 and i + 2 are in flight while slice i is
+// computed.  The x slice
 // (M rows x 512 bf16) arrives the same way into workgroup buffers of M
 // rows, its 16-byte pieces placed by an XOR of the row so that the 16
 // columns of one B-operand read fall in different banks: three buffers (x
@@ -35,6 +36,23 @@
 // (16 rows x 16 columns per wave) stays in registers over all of K and is
 // stored when the task's last slice is done: no cross-wave reduction.
 //
+// Tile layout (nb_tile_layout).  A one-time re-ordering of a layer for
+// this kernel: the blocks of 16 rows x 4 column blocks (one wave's slice)
+// are stored as the LDS image of a slot -- 3 KiB of indices, 2 KiB of
+// codebook in two arrays, rows rotated as above -- tile (g, s) at tile
+// index g * ceil(bpr / 4) + s, rows past N and blocks past bpr zero.  A
+// slice then arrives by five contiguous 1 KiB loads (the access shape
+// under which MI355X streams fastest) instead of 16 row pieces of 192 and
+// 128 bytes.  Within every 12-byte unit of 32 indices, index 4s + t
+// (s = 0..7, t = 0..3) is stored at index position o(s) + 8t,
+// o = (0, 1, 3, 4, 6, 7, 2, 5): the byte-class extraction of the M = 1
+// kernel (nb_stream_common.h, unit_selectors: 25 VALU ops per 32 indices)
+// then yields selector s = indices 4s .. 4s + 3 in natural order, and two
+// selectors are the 8 consecutive weights of one A operand -- 14.25 VALU
+// ops per 8 weights instead of 17 plus the per-group selector builds.
+// The MFMAs, their order and the x pieces are those of the reference
+// layout, so both layouts give the same bits.
+//
 // Weights are rounded to bf16 (RNE), as the reference's bf16 path;
 // accumulation is fp32.
 #include <algorithm>
@@ -42,6 +60,7 @@
 
 #include "nb_device.h"
 #include "nb_internal.h"
+#include "nb_stream_common.h"
 
 namespace nb {
 namespace {
@@ -50,7 +69,14 @@ typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 
-constexpr int kSkWaves = 8;
+// waves per workgroup and slots per wave ring
+#ifndef NB_SK_WAVES
+#define NB_SK_WAVES 8
+#endif
+#ifndef NB_SK_DEPTH
+#define NB_SK_DEPTH 3
+#endif
+constexpr int kSkWaves = NB_SK_WAVES;
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkRows = 16 * kSkWaves;         // rows of one task
 constexpr int kSkSliceK = 512;                 // K of one slice (4 blocks)
@@ -58,7 +84,7 @@ constexpr int kSkMaxM = 16;
 constexpr int kSkXRow = kSkSliceK * 2;         // LDS bytes of one staged x row
 constexpr int kSkIdxBytes = 16 * 192;          // indices of one slot
 constexpr int kSkSlot = kSkIdxBytes + 16 * 128;  // + codebooks
-constexpr int kSkDepth = 3;                    // slots per wave
+constexpr int kSkDepth = NB_SK_DEPTH;          // slots per wave
 constexpr int kSkRing = kSkWaves * kSkDepth * kSkSlot;
 constexpr int kSkLdsMax = 160 * 1024;
 static_assert(kSkRing + 2 * kSkMaxM * kSkXRow <= kSkLdsMax, "LDS");
@@ -68,6 +94,16 @@ static_assert(kSkSlot == 5 * 1024, "five 1 KiB loads per slot");
 __host__ __device__ constexpr int skinny_xbufs(int M) {
     return kSkRing + 3 * M * kSkXRow <= kSkLdsMax ? 3 : 2;
 }
+
+// Rotations of row r (0..15) of a slot: its 48-byte index blocks b sit at
+// block place (b + idx_rot(r)) & 3 of its 192 bytes, its 16-byte codebook
+// pieces p at place (p + cb_rot(r)) & 7 of its 128 bytes.  A ds_read_b128
+// of the compute side has the 16 lanes (q, r = 0..15) read one piece each
+// of the same block q: with these rotations the 16 pieces fall in 16
+// different 4-bank groups of the 64 banks, and each half of 8 lanes in 8
+// different groups of 32 banks.
+__host__ __device__ constexpr int idx_rot(int r) { return ((r >> 1) & 3) + (r >> 3); }
+__host__ __device__ constexpr int cb_rot(int r) { return (r & 6) | ((r ^ (r >> 3)) & 1); }
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
@@ -133,6 +169,38 @@ __device__ __forceinline__ void mfma_groups(const uint32_t (&d)[12], uint32_t lo
     }
 }
 
+// The same 16 MFMAs on the tile layout's index order: unit U (32 indices,
+// dwords d[3U .. 3U + 2]) gives groups 4U .. 4U + 3, selectors 2p and
+// 2p + 1 being the eight weights of group 4U + p in natural order.
+template <int U>
+__device__ __forceinline__ void mfma_units_tile(const uint32_t (&d)[12], uint32_t lo0,
+                                               uint32_t lo1, uint32_t hi0, uint32_t hi1,
+                                               const unsigned char* xrow, int piece0, int swz,
+                                               f32x4_t& acc) {
+    if constexpr (U < 4) {
+        uint32_t sel[8];
+        stream::unit_selectors(d[3 * U], d[3 * U + 1], d[3 * U + 2], sel);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sel[2 * p]);
+            const uint32_t ha = __builtin_amdgcn_perm(hi1, hi0, sel[2 * p]);
+            const uint32_t lb = __builtin_amdgcn_perm(lo1, lo0, sel[2 * p + 1]);
+            const uint32_t hb = __builtin_amdgcn_perm(hi1, hi0, sel[2 * p + 1]);
+            u32x4_t a;
+            a.x = __builtin_amdgcn_perm(ha, la, 0x05010400u);  // (w0, w1)
+            a.y = __builtin_amdgcn_perm(ha, la, 0x07030602u);  // (w2, w3)
+            a.z = __builtin_amdgcn_perm(hb, lb, 0x05010400u);  // (w4, w5)
+            a.w = __builtin_amdgcn_perm(hb, lb, 0x07030602u);  // (w6, w7)
+            const u32x4_t b =
+                *reinterpret_cast<const u32x4_t*>(xrow + 16 * ((piece0 + 4 * U + p) ^ swz));
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                          __builtin_bit_cast(bf16x8_t, b), acc,
+                                                          0, 0, 0);
+        }
+        mfma_units_tile<U + 1>(d, lo0, lo1, hi0, hi1, xrow, piece0, swz, acc);
+    }
+}
+
 // global_load_lds_dwordx4: 16 bytes per lane from `src` to
 // LDS address m0 + 16 * lane (m0 = the wave-uniform `lds`).  Completion is
 // tracked by vmcnt only; the compiler does not see the LDS write, so the
@@ -149,6 +217,25 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
 template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
+}
+
+// wait_vm for a wave-uniform n (a scalar branch to the immediate form;
+// n outside 1..24 waits for everything, which is always enough).
+__device__ __forceinline__ void wait_vm_n(int n) {
+    switch (n) {
+#define NB_SK_CASE(k) \
+    case k:           \
+        wait_vm<k>(); \
+        break;
+        NB_SK_CASE(1) NB_SK_CASE(2) NB_SK_CASE(3) NB_SK_CASE(4) NB_SK_CASE(5) NB_SK_CASE(6)
+        NB_SK_CASE(7) NB_SK_CASE(8) NB_SK_CASE(9) NB_SK_CASE(10) NB_SK_CASE(11) NB_SK_CASE(12)
+        NB_SK_CASE(13) NB_SK_CASE(14) NB_SK_CASE(15) NB_SK_CASE(16) NB_SK_CASE(17)
+        NB_SK_CASE(18) NB_SK_CASE(19) NB_SK_CASE(20) NB_SK_CASE(21) NB_SK_CASE(22)
+        NB_SK_CASE(23) NB_SK_CASE(24)
+#undef NB_SK_CASE
+        default:
+            wait_vm<0>();
+    }
 }
 
 // Workgroup barrier that waits for this wave's LDS operations only, not
@@ -217,7 +304,7 @@ __device__ __forceinline__ void cursor_next(const SkinnyArgs& a, Cursor& c, int 
     cursor_rows(a, c, wave);
 }
 
-template <int NXB>
+template <int NXB, bool TILE>
 __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
@@ -264,15 +351,15 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
 
     // Per-lane constants of the weight loads: load i < 3 (indices) puts
     // piece P = 64 i + lane of the slot at row P / 12, place P % 12, which
-    // holds piece (place - 3 rot) mod 12 of the row, rot = (row >> 1) & 3;
-    // load 3 + i (codebooks) puts P = 64 i + lane at row P / 8, place
-    // P % 8, holding piece (place - row) & 7.
+    // holds piece (place - 3 (idx_rot(row) & 3)) mod 12 of the row; load
+    // 3 + i (codebooks) puts P = 64 i + lane at row P / 8, place P % 8,
+    // holding piece (place - cb_rot(row)) & 7.
     int w_row[5], w_blk[5], w_off[5];
 #pragma unroll
     for (int i = 0; i < 3; ++i) {
         const int P = 64 * i + lane;
         const int rr = P / 12, place = P % 12;
-        const int piece = (place - 3 * ((rr >> 1) & 3) + 12) % 12;
+        const int piece = (place - 3 * (idx_rot(rr) & 3) + 12) % 12;
         w_row[i] = rr;
         w_blk[i] = piece / 3;
         w_off[i] = (piece % 3) * 16;
@@ -281,7 +368,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     for (int i = 0; i < 2; ++i) {
         const int P = 64 * i + lane;
         const int rr = P >> 3, place = P & 7;
-        const int piece = (place - rr) & 7;
+        const int piece = (place - cb_rot(rr)) & 7;
         w_row[3 + i] = rr;
         w_blk[3 + i] = piece >> 1;
         w_off[3 + i] = (piece & 1) * 16;
@@ -302,26 +389,43 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         wtask = c.task;
     };
     auto issue_w = [&](const Cursor& c, int slot) {
-        if (c.task != wtask) w_rows(c);
         const uint32_t dst = __builtin_amdgcn_readfirstlane(ring + slot * kSkSlot);
+        if constexpr (TILE) {
+            // the slot's image: tile (group, slice), groups past the
+            // layer's last read its last (their rows are not stored)
+            const int64_t g = min(c.row0 >> 4, (c.N - 1) >> 4);
+            const int64_t tile = g * c.ns + c.s;
+            const unsigned char* ib = c.packed + tile * kSkIdxBytes + 16 * lane;
+            const unsigned char* cp =
+                reinterpret_cast<const unsigned char*>(c.cb) + tile * (kSkSlot - kSkIdxBytes) +
+                16 * lane;
+            dma16(dst, ib);
+            dma16(dst + 1024, ib + 1024);
+            dma16(dst + 2048, ib + 2048);
+            dma16(dst + 3072, cp);
+            dma16(dst + 4096, cp + 1024);
+        } else {
+            if (c.task != wtask) w_rows(c);
 #pragma unroll
-        for (int i = 0; i < 5; ++i) {
-            const int blk = min(4 * c.s + w_blk[i], c.bpr - 1);
-            dma16(dst + 1024 * i, wbase[i] + blk * (i < 3 ? 48 : 32));
+            for (int i = 0; i < 5; ++i) {
+                const int blk = min(4 * c.s + w_blk[i], c.bpr - 1);
+                dma16(dst + 1024 * i, wbase[i] + blk * (i < 3 ? 48 : 32));
+            }
         }
     };
     // x slice of item c into buffer `buf`: wave w loads activation rows
     // min(2w + j, M - 1), j = 0, 1 -- always two loads, so the wait counts
     // below are exact (a clamped row rewrites row M - 1 with the same bytes,
     // before anyone reads that buffer).  Lane l takes the 16 bytes of
-    // column piece l ^ (m & 7), so piece p of row m sits at place
-    // p ^ (m & 7): the 16 rows of one B-operand read fall in different
-    // banks.  Columns past K repeat the last 8 (their weights are zero).
+    // column piece l ^ (m & 15), so piece p of row m sits at place
+    // p ^ (m & 15): the 16 rows of one B-operand read fall in 16 different
+    // 4-bank groups (and each 8 of them in 8 groups of 32 banks).  Columns
+    // past K repeat the last 8 (their weights are zero).
     auto issue_x = [&](const Cursor& c, int buf) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int m = min(2 * wave + j, M - 1);
-            const int piece = lane ^ (m & 7);
+            const int piece = lane ^ (m & 15);
             const int k = min(c.s * kSkSliceK + piece * 8, c.K - 8);
             dma16(__builtin_amdgcn_readfirstlane(base + kSkRing + buf * xbuf_bytes + m * kSkXRow),
                   c.x + (int64_t)m * c.K + k);
@@ -331,11 +435,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     // MFMA column r reads activation row min(r, M - 1)
     const int xm = r < M ? r : M - 1;
     // this lane's pieces of a slot (rotated places, see above)
-    const int idx_off = r * 192 + ((q + (r >> 1)) & 3) * 48;
-    const int cb_off0 = kSkIdxBytes + r * 128 + ((2 * q + r) & 7) * 16;
-    const int cb_off1 = kSkIdxBytes + r * 128 + ((2 * q + 1 + r) & 7) * 16;
+    const int idx_off = r * 192 + ((q + idx_rot(r)) & 3) * 48;
+    const int cb_off0 = kSkIdxBytes + r * 128 + ((2 * q + cb_rot(r)) & 7) * 16;
+    const int cb_off1 = kSkIdxBytes + r * 128 + ((2 * q + 1 + cb_rot(r)) & 7) * 16;
     const int x_off = xm * kSkXRow;
-    const int x_swz = xm & 7;
+    const int x_swz = xm & 15;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
     // A finished task's outputs wait in `pend` and are stored after the
     // next item's loads are issued.  acc lane (q, r) holds C[4q + v][r]:
@@ -366,50 +470,48 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     };
 
     // ---- the pipeline -----------------------------------------------------
-    // Loads complete in issue order.  With three x buffers the issue order
-    // is X(0) W(0) X(1) W(1), then item i issues X(i + 2) W(i + 2) after its
-    // barrier, and W(i), X(i) are in once at most the 7 loads of X(i + 1)
-    // and W(i + 1) are outstanding.  With two, the order is X(0) W(0) W(1),
-    // then item i issues X(i + 1) W(i + 2), and W(i), X(i) are in once at
-    // most the 5 loads of W(i + 1) are.  Either way the weights are
-    // requested two items ahead.  (Output stores, issued after an item's
-    // loads, only make the next wait longer.)
-    constexpr int kLead = NXB == 3 ? 2 : 1;  // items between X's issue and use
-    constexpr int kAfter = NXB == 3 ? 7 : 5;
+    // Item i's loads are X(i) (the x slice, two loads, into buffer
+    // i % NXB) and W(i) (the wave's weight slice, five loads, into slot
+    // i % kSkDepth).  Step j (j = -kSkDepth .. -1 before the loop, then
+    // item j's step) issues X(j + kLead), then W(j + kSkDepth), where they
+    // exist.  Item i's step waits until W(i) and X(i) are in, passes the
+    // workgroup barrier (every wave's x pieces of item i are in, and every
+    // wave is done with item i - 1, whose x buffer X(i + kLead) refills),
+    // reads slot i into registers, issues its loads -- W(i + kSkDepth)
+    // into the slot just read -- and computes.  kSkDepth slices of weights
+    // are in flight while one is computed.  Loads complete in issue order,
+    // so W(i) and X(i) are in once at most after(i) loads are outstanding:
+    // those issued after X(i) (the later of the two; kLead <= kSkDepth).
+    // (Output stores, issued after an item's loads, only make the waits
+    // longer.)
+    constexpr int kLead = NXB - 1;  // steps between X's issue and use
+    static_assert(kLead <= kSkDepth, "x is requested no earlier than the weights");
+    auto after = [&](int i) {
+        const int j0 = i - kLead;  // the step that issued X(i)
+        int n = (kLead < kSkDepth && j0 + kSkDepth < nitems) ? 5 : 0;
+        for (int j = j0 + 1; j < i; ++j) {
+            n += (j + kLead < nitems ? 2 : 0) + (j + kSkDepth < nitems ? 5 : 0);
+        }
+        return n;
+    };
     Cursor cx = cc, cw = cc;
-    issue_x(cx, 0);
-    cursor_next(a, cx, wave);
-    issue_w(cw, 0);
-    cursor_next(a, cw, wave);
-    if (nitems > 1) {
-        if (NXB == 3) {
-            issue_x(cx, 1);
+    for (int j = -kSkDepth; j < 0; ++j) {
+        if (j + kLead >= 0 && j + kLead < nitems) {
+            issue_x(cx, (j + kLead) % NXB);
             cursor_next(a, cx, wave);
         }
-        issue_w(cw, 1);
-        cursor_next(a, cw, wave);
+        if (j + kSkDepth < nitems) {
+            issue_w(cw, j + kSkDepth);
+            cursor_next(a, cw, wave);
+        }
     }
 
     for (int i = 0; i < nitems; ++i) {
-        if (i + 1 < nitems) {
-            wait_vm<kAfter>();
-        } else {
-            wait_vm<0>();
-        }
-        // every wave's x pieces of item i are in, and every wave is done
-        // with item i - 1 (the buffers the next loads overwrite)
+        wait_vm_n(after(i));
         wg_barrier();
-        if (i + kLead < nitems) {
-            issue_x(cx, (i + kLead) % NXB);
-            cursor_next(a, cx, wave);
-        }
-        if (i + 2 < nitems) {
-            issue_w(cw, (i + 2) % kSkDepth);
-            cursor_next(a, cw, wave);
-        }
-        if (pending) store();
-        // ---- compute slice cc.s of the task ----
-        const unsigned char* slot = ring_p + (i % kSkDepth) * kSkSlot;
+        // ---- slot i into registers, then this step's loads ----
+        const int si = i % kSkDepth;
+        const unsigned char* slot = ring_p + si * kSkSlot;
         uint32_t d[12];
         {
             const u32x4_t* ip = reinterpret_cast<const u32x4_t*>(slot + idx_off);
@@ -424,6 +526,18 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         }
         const f32x4_t c0 = *reinterpret_cast<const f32x4_t*>(slot + cb_off0);
         const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(slot + cb_off1);
+        // the slot's bytes are in registers before its refill is issued
+        asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+        if (i + kLead < nitems) {
+            issue_x(cx, (i + kLead) % NXB);
+            cursor_next(a, cx, wave);
+        }
+        if (i + kSkDepth < nitems) {
+            issue_w(cw, si);
+            cursor_next(a, cw, wave);
+        }
+        if (pending) store();
+        // ---- compute slice cc.s of the task ----
         const bool live = cc.row0 + r < cc.N && 4 * cc.s + q < cc.bpr;
         const uint32_t p0 = pack_bf16x2(c0.x, c0.y);
         const uint32_t p1 = pack_bf16x2(c0.z, c0.w);
@@ -438,7 +552,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         lo1 = live ? lo1 : 0u;
         hi1 = live ? hi1 : 0u;
         const unsigned char* xb = smem + kSkRing + (i % NXB) * xbuf_bytes + x_off;
-        mfma_groups<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+        if constexpr (TILE) {
+            mfma_units_tile<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+        } else {
+            mfma_groups<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+        }
         if (cc.s == cc.ns - 1) {
             pend = acc;
             pend_p = cc.p;
@@ -452,10 +570,104 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     if (pending) store();
 }
 
+// Index position of index i (= 4s + t) of a 32-index unit in the tile
+// layout: o(s) + 8t, o(s) = stream::sel_offset(s).
+__host__ __device__ constexpr int sel_position(int i) {
+    return stream::sel_offset(i >> 2) + 8 * (i & 3);
+}
+
+// 3-bit field at index position i of a 12-byte unit (dwords u[0..2])
+template <int I>
+__device__ __forceinline__ uint32_t unit_field(const uint32_t* u) {
+    constexpr int bit = 3 * I, w = bit >> 5, off = bit & 31;
+    if constexpr (off <= 29) {
+        return (u[w] >> off) & 7u;
+    } else {
+        return ((u[w] >> off) | (u[w + 1] << (32 - off))) & 7u;
+    }
+}
+
+template <int I>
+__device__ __forceinline__ void unit_put(uint32_t* u, uint32_t f) {
+    constexpr int bit = 3 * I, w = bit >> 5, off = bit & 31;
+    u[w] |= f << off;
+    if constexpr (off > 29) u[w + 1] |= f >> (32 - off);
+}
+
+template <int I>
+__device__ __forceinline__ void sel_unit(const uint32_t* in, uint32_t* out) {
+    if constexpr (I < 32) {
+        unit_put<sel_position(I)>(out, unit_field<I>(in));
+        sel_unit<I + 1>(in, out);
+    }
+}
+
+// One thread per block place of a tile (64 per tile: row rr, block blk of
+// the slice): the block's 48 index bytes in selector order at the rotated
+// place the kernel's slot holds them, its 8 codebook entries as two
+// rotated 16-byte pieces; zeros where the row or block is past the layer.
+__global__ __launch_bounds__(256) void tile_layout_kernel(const uint8_t* packed,
+                                                          const float* codebook, int N, int bpr,
+                                                          int ns, int64_t nthreads, uint8_t* tp,
+                                                          float* tc) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= nthreads) return;
+    const int64_t tile = t >> 6;
+    const int rr = (int)(t >> 2) & 15, blk = (int)t & 3;
+    const int64_t row = tile / ns * 16 + rr;
+    const int kb = (int)(tile % ns) * 4 + blk;
+    uint32_t o[12] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+    u32x4_t c0 = {0u, 0u, 0u, 0u}, c1 = c0;
+    if (row < N && kb < bpr) {
+        const int64_t b = row * bpr + kb;
+        const u32x4_t* src = reinterpret_cast<const u32x4_t*>(packed + b * 48);
+        uint32_t d[12];
+#pragma unroll
+        for (int v = 0; v < 3; ++v) {
+            const u32x4_t u = src[v];
+            d[4 * v] = u.x;
+            d[4 * v + 1] = u.y;
+            d[4 * v + 2] = u.z;
+            d[4 * v + 3] = u.w;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sel_unit<0>(d + 3 * u, o + 3 * u);
+        const u32x4_t* cs = reinterpret_cast<const u32x4_t*>(codebook + b * 8);
+        c0 = cs[0];
+        c1 = cs[1];
+    }
+    u32x4_t* di = reinterpret_cast<u32x4_t*>(tp + tile * kSkIdxBytes + rr * 192 +
+                                             ((blk + idx_rot(rr)) & 3) * 48);
+#pragma unroll
+    for (int v = 0; v < 3; ++v) {
+        di[v] = u32x4_t{o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]};
+    }
+    unsigned char* dc = reinterpret_cast<unsigned char*>(tc) + tile * (kSkSlot - kSkIdxBytes) +
+                        rr * 128;
+    *reinterpret_cast<u32x4_t*>(dc + ((2 * blk + cb_rot(rr)) & 7) * 16) = c0;
+    *reinterpret_cast<u32x4_t*>(dc + ((2 * blk + 1 + cb_rot(rr)) & 7) * 16) = c1;
+}
+
 }  // namespace
 
+int64_t tile_layout_tiles(int N, int K) {
+    return (int64_t)((N + 15) / 16) * ((K / 128 + 3) / 4);
+}
+
+int launch_tile_layout(const uint8_t* packed, const float* codebook, int N, int K,
+                       uint8_t* tpacked, float* tcodebook, hipStream_t stream) {
+    const int64_t nthreads = tile_layout_tiles(N, K) * 64;
+    if (nthreads == 0) return NB_OK;
+    const int64_t grid = (nthreads + 255) / 256;
+    if (grid > 0x7fffffff) return fail(NB_EUNSUPPORTED, "nb_tile_layout: layer too large");
+    hipLaunchKernelGGL(tile_layout_kernel, dim3((unsigned)grid), dim3(256), 0, stream, packed,
+                       codebook, N, K / 128, (K / 128 + 3) / 4, nthreads, tpacked, tcodebook);
+    return check_launch("nb_tile_layout");
+}
+
 int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host_probs,
-                       int nprob, int M, int y_dtype, hipStream_t stream) {
+                       int nprob, int M, int y_dtype, bool tile, hipStream_t stream) {
+    const char* fn = tile ? "nb_gemm_skinny_tile_batched" : "nb_gemm_skinny_batched";
     const int cus = std::max(1, std::min(device_cu_count(), kStreamMaxGroups));
     // launches of at most kSkinnyMaxProbs problems each
     for (int p0 = 0; p0 < nprob; p0 += kSkinnyMaxProbs) {
@@ -478,7 +690,7 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
             for (int t = 0; t < nt; ++t) slices.push_back(ns);
             total_slices += (int64_t)nt * ns;
             if (slices.size() > (size_t)0x7fffffff) {
-                return fail(NB_EUNSUPPORTED, "nb_gemm_skinny_batched: too many rows");
+                return fail(NB_EUNSUPPORTED, "%s: too many rows", fn);
             }
         }
         const int ntask = (int)slices.size();
@@ -496,14 +708,12 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
             A.wg_task0[g] = g == G ? ntask : t;
         }
         const size_t lds = (size_t)kSkRing + (size_t)skinny_xbufs(M) * M * kSkXRow;
-        if (skinny_xbufs(M) == 3) {
-            hipLaunchKernelGGL(gemv_skinny_kernel<3>, dim3((unsigned)G), dim3(kSkThreads), lds,
-                               stream, A);
-        } else {
-            hipLaunchKernelGGL(gemv_skinny_kernel<2>, dim3((unsigned)G), dim3(kSkThreads), lds,
-                               stream, A);
-        }
-        const int st = check_launch("nb_gemm_skinny_batched");
+        auto kernel = skinny_xbufs(M) == 3 ? (tile ? gemv_skinny_kernel<3, true>
+                                                   : gemv_skinny_kernel<3, false>)
+                                           : (tile ? gemv_skinny_kernel<2, true>
+                                                   : gemv_skinny_kernel<2, false>);
+        hipLaunchKernelGGL(kernel, dim3((unsigned)G), dim3(kSkThreads), lds, stream, A);
+        const int st = check_launch(fn);
         if (st) return st;
     }
     return NB_OK;

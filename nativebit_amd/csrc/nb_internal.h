@@ -94,8 +94,14 @@ int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host
 
 // Launches the batched skinny GEMM (M <= 16 activation rows) over the
 // problem table.
+// tile: items are in the tile layout (nb_tile_layout).
 int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host_probs,
-                       int nprob, int M, int y_dtype, hipStream_t stream);
+                       int nprob, int M, int y_dtype, bool tile, hipStream_t stream);
+// Tiles (16 rows x 4 column blocks) of an N x K layer's tile layout, and
+// the launch that writes it (3072 index bytes and 512 floats per tile).
+int64_t tile_layout_tiles(int N, int K);
+int launch_tile_layout(const uint8_t* packed, const float* codebook, int N, int K,
+                       uint8_t* tpacked, float* tcodebook, hipStream_t stream);
 
 // The batched skinny GEMM for M <= 4 on the row-quad layout
 // (nb_gemv_quad.hip); gemv_quad_supported says whether the batch is in its

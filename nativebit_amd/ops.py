@@ -160,7 +160,9 @@ class GemvBatch:
 
     ``layout="quad"`` (m <= 4, K >= 2048): every item's packed / codebook
     are the row-quad layout of its layer (``quad_layout``), run by
-    nb_gemm_skinny_quad_batched.
+    nb_gemm_skinny_quad_batched.  ``layout="tile"`` (m > 1): every item's
+    packed / codebook are the tile layout of its layer (``tile_layout``),
+    run by nb_gemm_skinny_tile_batched.
 
     The device table is built once here; each run() enqueues one launch on
     torch's current stream (graph-capturable).  The tensors are referenced
@@ -170,10 +172,12 @@ class GemvBatch:
     def __init__(self, items, m: int = 1, layout: str = "rows"):
         if not 1 <= m <= 16:
             raise ValueError(f"m={m} outside 1..16")
-        if layout not in ("rows", "quad"):
+        if layout not in ("rows", "quad", "tile"):
             raise ValueError(f"unknown layout {layout!r}")
         if layout == "quad" and m > 4:
             raise ValueError(f"the row-quad kernel takes m <= 4 (got {m})")
+        if layout == "tile" and m < 2:
+            raise ValueError("the tile layout is for m > 1 (the skinny kernel)")
         self.m = int(m)
         self.layout = layout
         self.items = list(items)
@@ -222,9 +226,12 @@ class GemvBatch:
                                      "bfloat16 y")
             if packed.dtype != torch.uint8 or cb.dtype != torch.float32:
                 raise TypeError(f"item {i}: packed must be uint8 and codebook float32")
-            rows = (N + 3) // 4 * 4 if layout == "quad" else N
-            if cb.shape != (rows * K // 128, 8) or packed.numel() < packed_nbytes(rows * K, 3):
-                what = "row-quad layout of a" if layout == "quad" else "a"
+            if layout == "tile":
+                nblk = (N + 15) // 16 * 16 * ((K // 128 + 3) // 4 * 4)
+            else:
+                nblk = ((N + 3) // 4 * 4 if layout == "quad" else N) * K // 128
+            if cb.shape != (nblk, 8) or packed.numel() < nblk * 48:
+                what = {"quad": "row-quad layout of a", "tile": "tile layout of a"}.get(layout, "a")
                 raise ValueError(f"item {i}: not {what} 3-bit / 8-entry / block-128 {N}x{K} "
                                  "layer")
             if layout == "quad" and K < 2048:
@@ -255,6 +262,10 @@ class GemvBatch:
         lib = _lib.load()
         if self.layout == "quad":
             _lib.check(lib.nb_gemm_skinny_quad_batched(self._arr, self.table.data_ptr(),
+                                                       self.count, self.m, _DT[self.y_dtype],
+                                                       stream))
+        elif self.layout == "tile":
+            _lib.check(lib.nb_gemm_skinny_tile_batched(self._arr, self.table.data_ptr(),
                                                        self.count, self.m, _DT[self.y_dtype],
                                                        stream))
         elif self.m == 1:
@@ -288,6 +299,32 @@ def quad_layout(packed: torch.Tensor, codebook: torch.Tensor, N: int, K: int):
     _lib.check(lib.nb_quad_layout(packed.data_ptr(), codebook.data_ptr(), N, K, qp.data_ptr(),
                                   qc.data_ptr(), _stream(packed)))
     return qp, qc
+
+
+def tile_layout(packed: torch.Tensor, codebook: torch.Tensor, N: int, K: int):
+    """The tile layout of a 3-bit / 8-entry / block-128 N x K layer
+    (nb_tile_layout): tiles of 16 rows x 4 column blocks (rows and column
+    blocks padded with zero blocks), each stored as the skinny kernel's LDS
+    slot holds it, indices in selector order.  Returns (tpacked uint8,
+    tcodebook (tiles * 64, 8) float32) on the layer's device, for
+    GemvBatch(..., layout="tile")."""
+    for name, t in (("packed", packed), ("codebook", codebook)):
+        _require_cuda(name, t)
+    _same_device(packed, codebook)
+    if packed.dtype != torch.uint8 or codebook.dtype != torch.float32:
+        raise TypeError("packed must be uint8 and codebook float32")
+    if N < 0 or K <= 0 or K % 128 or codebook.shape != (N * K // 128, 8) or \
+            packed.numel() < packed_nbytes(N * K, 3):
+        raise ValueError(f"not a 3-bit / 8-entry / block-128 {N}x{K} layer")
+    if not packed.is_contiguous() or not codebook.is_contiguous():
+        raise ValueError("packed and codebook must be contiguous")
+    lib = _lib.load()
+    nbytes = int(lib.nb_tile_layout_bytes(N, K))
+    tp = torch.empty(nbytes, dtype=torch.uint8, device=packed.device)
+    tc = torch.empty((nbytes // 48, 8), dtype=torch.float32, device=packed.device)
+    _lib.check(lib.nb_tile_layout(packed.data_ptr(), codebook.data_ptr(), N, K, tp.data_ptr(),
+                                  tc.data_ptr(), _stream(packed)))
+    return tp, tc
 
 
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,

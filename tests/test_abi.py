@@ -295,6 +295,38 @@ def test_quad_batch_and_layout_validation():
     assert ql(None, None, 0, 256, None, None, None) == _lib.NB_OK
 
 
+def test_tile_batch_and_layout_validation():
+    """nb_gemm_skinny_tile_batched: the skinny checks (M 1..16) under its
+    own name; nb_tile_layout: shape, pointers and alignment; the layout's
+    byte count (ceil(N / 16) * ceil(K / 512) tiles of 3072 index bytes)."""
+    lib = _lib.load()
+    Item = _lib.BatchItem
+    good = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 256))
+    ts = lib.nb_gemm_skinny_tile_batched
+    for M in (0, 17):
+        assert ts(good, FAKE, 1, M, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert _lib.last_error().startswith("nb_gemm_skinny_tile_batched")
+    assert ts(good, None, 1, 8, _lib.NB_F32, None) == _lib.NB_EINVAL
+    assert ts((Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 200)), FAKE, 1, 8, _lib.NB_F32,
+              None) == _lib.NB_EUNSUPPORTED
+    add16 = (Item * 1)(Item(FAKE, FAKE, FAKE, FAKE, 32, 256, 0, _lib.NB_Y_ADD, None, 0.0, 0))
+    assert ts(add16, FAKE, 1, 8, _lib.NB_BF16, None) == _lib.NB_EUNSUPPORTED
+    empty = (Item * 1)(Item(None, None, None, None, 0, 256))
+    assert ts(empty, None, 1, 8, _lib.NB_F32, None) == _lib.NB_OK
+    assert lib.nb_tile_layout_bytes(16, 2048) == 4 * 3072
+    assert lib.nb_tile_layout_bytes(17, 6912) == 2 * 14 * 3072
+    assert lib.nb_tile_layout_bytes(0, 256) == 0 and lib.nb_tile_layout_bytes(4, 200) == 0
+    tl = lib.nb_tile_layout
+    for N, K in ((8, 200), (8, 0), (-1, 256)):
+        assert tl(FAKE, FAKE, N, K, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert _lib.last_error().startswith("nb_tile_layout")
+    assert tl(None, FAKE, 8, 256, FAKE, FAKE, None) == _lib.NB_EINVAL
+    assert tl(FAKE, FAKE, 8, 256, FAKE, None, None) == _lib.NB_EINVAL
+    assert tl(FAKE + 8, FAKE, 8, 256, FAKE, FAKE, None) == _lib.NB_EALIGN
+    assert tl(FAKE, FAKE, 8, 256, FAKE, FAKE + 4, None) == _lib.NB_EALIGN
+    assert tl(None, None, 0, 256, None, None, None) == _lib.NB_OK
+
+
 # --- prefill and decode-step entry points: host-side validation -------------
 
 def prefill(**kw):
