@@ -212,6 +212,14 @@ __device__ __forceinline__ void dma16(uint32_t lds, const void* src) {
                  : "memory", "m0");
 }
 
+// The same load marked non-temporal: weights are read once per launch.
+__device__ __forceinline__ void dma16_nt(uint32_t lds, const void* src) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off nt"
+                 :
+                 : "s"(lds), "v"(src)
+                 : "memory", "m0");
+}
+
 // Waits until at most N vector-memory operations of this wave are
 // outstanding (they complete in issue order).
 template <int N>
@@ -399,11 +407,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             const unsigned char* cp =
                 reinterpret_cast<const unsigned char*>(c.cb) + tile * (kSkSlot - kSkIdxBytes) +
                 16 * lane;
-            dma16(dst, ib);
-            dma16(dst + 1024, ib + 1024);
-            dma16(dst + 2048, ib + 2048);
-            dma16(dst + 3072, cp);
-            dma16(dst + 4096, cp + 1024);
+            dma16_nt(dst, ib);
+            dma16_nt(dst + 1024, ib + 1024);
+            dma16_nt(dst + 2048, ib + 2048);
+            dma16_nt(dst + 3072, cp);
+            dma16_nt(dst + 4096, cp + 1024);
         } else {
             if (c.task != wtask) w_rows(c);
 #pragma unroll
@@ -678,10 +686,13 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
         A.tasks.nprob = n;
         A.M = M;
         A.y_dtype = y_dtype;
-        // tasks and their slice counts, then contiguous task ranges of about
-        // equal slice count, one per workgroup
+        // tasks and their slice counts, then contiguous task ranges, one per
+        // workgroup, whose largest slice count is the least possible: the
+        // smallest capacity C for which filling workgroups in order up to C
+        // slices needs at most G of them (binary search), then that filling
         std::vector<int> slices;
         int64_t total_slices = 0;
+        int max_slices = 0;
         for (int i = 0; i < n; ++i) {
             A.tasks.task_begin[i] = (int32_t)slices.size();
             const StreamProblem& P = host_probs[p0 + i];
@@ -689,6 +700,7 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
             const int ns = ((P.K >> 7) + 3) >> 2;
             for (int t = 0; t < nt; ++t) slices.push_back(ns);
             total_slices += (int64_t)nt * ns;
+            max_slices = std::max(max_slices, ns);
             if (slices.size() > (size_t)0x7fffffff) {
                 return fail(NB_EUNSUPPORTED, "%s: too many rows", fn);
             }
@@ -696,23 +708,42 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
         const int ntask = (int)slices.size();
         if (ntask == 0) continue;
         const int G = std::min(cus, ntask);
-        int t = 0;
-        int64_t acc = 0;
-        A.wg_task0[0] = 0;
-        for (int g = 1; g <= G; ++g) {
-            const int64_t goal = total_slices * g / G;
-            // (a task goes to the workgroup that holds its midpoint)
-            while (t < ntask && 2 * acc + slices[t] <= 2 * goal) acc += slices[t++];
-            // every workgroup keeps at least one task while tasks remain
-            if (t == A.wg_task0[g - 1] && t < ntask) acc += slices[t++];
-            A.wg_task0[g] = g == G ? ntask : t;
+        auto groups_for = [&](int64_t cap) {
+            int g = 1;
+            int64_t acc = 0;
+            for (int t = 0; t < ntask; ++t) {
+                if (acc + slices[t] > cap) {
+                    ++g;
+                    acc = 0;
+                }
+                acc += slices[t];
+            }
+            return g;
+        };
+        int64_t lo = std::max<int64_t>(max_slices, (total_slices + G - 1) / G), hi = total_slices;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) / 2;
+            if (groups_for(mid) <= G) hi = mid; else lo = mid + 1;
+        }
+        int used = 0;
+        {
+            int64_t acc = 0;
+            A.wg_task0[0] = 0;
+            for (int t = 0; t < ntask; ++t) {
+                if (acc + slices[t] > lo) {
+                    A.wg_task0[++used] = t;
+                    acc = 0;
+                }
+                acc += slices[t];
+            }
+            A.wg_task0[++used] = ntask;
         }
         const size_t lds = (size_t)kSkRing + (size_t)skinny_xbufs(M) * M * kSkXRow;
         auto kernel = skinny_xbufs(M) == 3 ? (tile ? gemv_skinny_kernel<3, true>
                                                    : gemv_skinny_kernel<3, false>)
                                            : (tile ? gemv_skinny_kernel<2, true>
                                                    : gemv_skinny_kernel<2, false>);
-        hipLaunchKernelGGL(kernel, dim3((unsigned)G), dim3(kSkThreads), lds, stream, A);
+        hipLaunchKernelGGL(kernel, dim3((unsigned)used), dim3(kSkThreads), lds, stream, A);
         const int st = check_launch(fn);
         if (st) return st;
     }
