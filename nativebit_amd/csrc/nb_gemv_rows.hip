@@ -158,8 +158,9 @@ void gemv_rows_kernel(RowsArgs a) {
         dma16<0>(dst + kSlotIdx + 1024, min(cp + 1024, clast));
     };
     // One chunk's loads go out behind the activation pieces, the other slots'
-    // once the pieces are in: the pieces (which every workgroup needs before
-    // it can compute) then do not queue behind the whole weight burst.
+    // once the activations are staged: the pieces (which every workgroup
+    // needs before it can compute) then do not queue behind the whole weight
+    // burst, and no load issue stalls a wave between the barriers below.
     const int first = min(n, SLOTS);
     const int early = min(first, 1);
     for (int i = 0; i < early; ++i) issue(c0 + wave + i * kWaves, i);
@@ -167,7 +168,6 @@ void gemv_rows_kernel(RowsArgs a) {
     // ---- 3. activations: wait for their pieces (the weights stay in flight),
     //         form them in fp32, round to bf16, stage in the selector layout
     wait_vm_n<SLOTS * kLoads>(early * kLoads);
-    for (int i = early; i < first; ++i) issue(c0 + wave + i * kWaves, i);
     typedef __attribute__((ext_vector_type(4))) float f4;
     if constexpr (XMODE == NB_X_RMSNORM) {
         // the norm's sum of squares over this wave's own pieces of x (in LDS
@@ -183,61 +183,72 @@ void gemv_rows_kernel(RowsArgs a) {
         if (lane == 0) red[wave] = ssw;
     }
     __syncthreads();  // every wave's pieces (and partial sums) are in LDS
-    const int ng = K >> 3;
-    constexpr int kMaxG = (kMaxK / 8 + kThreads - 1) / kThreads;
     uint16_t* xh = reinterpret_cast<uint16_t*>(xs);
     if constexpr (XMODE == NB_X_BF16) {
-#pragma unroll
-        for (int j = 0; j < kMaxG; ++j) {
-            const int g = tid + j * kThreads;
-            if (g < ng) {
-                uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    col[staged_half(g & 15, e)] = reinterpret_cast<const uint16_t*>(raw)[8 * g + e];
-            }
+        // one thread per 32-element unit: its 64 bytes in four 16-byte
+        // reads, the staged unit's four 16-byte pieces in four writes (one
+        // LDS round trip; element by element, each write would wait for its
+        // read)
+        for (int u = tid; u < (K >> 5); u += kThreads) {
+            const u32x4_t* src = reinterpret_cast<const u32x4_t*>(raw + 64 * u);
+            const u32x4_t r0 = src[0], r1 = src[1], r2 = src[2], r3 = src[3];
+            const uint32_t w[16] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y, r1.z, r1.w,
+                                    r2.x, r2.y, r2.z, r2.w, r3.x, r3.y, r3.z, r3.w};
+            stage_unit(xs + (u >> 2) * kXColBytes, u & 3, w);
         }
     } else {
-        // each thread's groups of 8 inputs, read once into registers
+        // quarter groups of 4 inputs per thread (each thread's divisions
+        // are its critical path), read into registers before any is used
+        const int nq = K >> 2;
+        constexpr int kMaxQ = (kMaxK / 4 + kThreads - 1) / kThreads;
         const f4* xf4 = reinterpret_cast<const f4*>(raw);
         const f4* sf4 = reinterpret_cast<const f4*>(raw + a.raw_bytes / 2);
-        f4 xr[kMaxG][2], sr[kMaxG][2];
+        f4 xr[kMaxQ], sr[kMaxQ];
 #pragma unroll
-        for (int j = 0; j < kMaxG; ++j) {
-            const int g = tid + j * kThreads;
-            const int gg = g < ng ? g : 0;
-            xr[j][0] = xf4[2 * gg];
-            xr[j][1] = xf4[2 * gg + 1];
-            sr[j][0] = sf4[2 * gg];
-            sr[j][1] = sf4[2 * gg + 1];
+        for (int j = 0; j < kMaxQ; ++j) {
+            const int q = tid + j * kThreads;
+            const int qq = q < nq ? q : 0;
+            xr[j] = xf4[qq];
+            sr[j] = sf4[qq];
         }
         float norm = 1.f;
         if constexpr (XMODE == NB_X_RMSNORM) {
+            // the waves' partial sums, added in wave order in every thread
+            const f4 r0 = reinterpret_cast<const f4*>(red)[0];
+            const f4 r1 = reinterpret_cast<const f4*>(red)[1];
+            const f4 r2 = reinterpret_cast<const f4*>(red)[2];
+            static_assert(kWaves == 12, "three vectors of partial sums");
+            const float rw[12] = {r0.x, r0.y, r0.z, r0.w, r1.x, r1.y,
+                                  r1.z, r1.w, r2.x, r2.y, r2.z, r2.w};
             float t = 0.f;
-            for (int w = 0; w < kWaves; ++w) t += red[w];  // same order in every thread
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) t += rw[w];
             norm = sqrtf(t / (float)K + a.eps);
         }
 #pragma unroll
-        for (int j = 0; j < kMaxG; ++j) {
-            const int g = tid + j * kThreads;
-            if (g < ng) {
+        for (int j = 0; j < kMaxQ; ++j) {
+            const int q = tid + j * kThreads;
+            if (q < nq) {
+                const int g = q >> 1, e0 = 4 * (q & 1);
                 uint16_t* col = xh + (g >> 4) * (kXColBytes / 2);
-                const float xv[8] = {xr[j][0].x, xr[j][0].y, xr[j][0].z, xr[j][0].w,
-                                     xr[j][1].x, xr[j][1].y, xr[j][1].z, xr[j][1].w};
-                const float sv[8] = {sr[j][0].x, sr[j][0].y, sr[j][0].z, sr[j][0].w,
-                                     sr[j][1].x, sr[j][1].y, sr[j][1].z, sr[j][1].w};
+                const float xv[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+                const float sv[4] = {sr[j].x, sr[j].y, sr[j].z, sr[j].w};
 #pragma unroll
-                for (int e = 0; e < 8; ++e) {
+                for (int e = 0; e < 4; ++e) {
                     // RMSNorm.forward's (x / norm) * w, generate_torch.py:37; silu(g) * u,
                     // 116-117 (exp(-g) by v_exp_f32, a few ulp, below the bf16 rounding)
                     const float r = XMODE == NB_X_RMSNORM ? (xv[e] / norm) * sv[e]
                                                           : (xv[e] / (1.0f + __expf(-xv[e]))) * sv[e];
-                    col[staged_half(g & 15, e)] = f32_to_bf16_rne(r);
+                    col[staged_half(g & 15, e0 + e)] = f32_to_bf16_rne(r);
                 }
             }
         }
     }
     __syncthreads();
+    // the wave's other first chunks go out now: issued before the staging,
+    // their loads stall behind the memory system's queue and hold up the
+    // barriers above
+    for (int i = early; i < first; ++i) issue(c0 + wave + i * kWaves, i);
 
     // ---- 4. the wave's chunks: wait, read the slot, refill it, compute ------
     // Lane l takes column block l % bpr of row l / bpr of every chunk (lanes
