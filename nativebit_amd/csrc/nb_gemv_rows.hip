@@ -253,13 +253,9 @@ void gemv_rows_kernel(RowsArgs a) {
     // ---- 4. the wave's chunks: wait, read the slot, refill it, compute ------
     // Lane l takes column block l % bpr of row l / bpr of every chunk (lanes
     // past R * bpr compute a block nobody reads), so its activation units
-    // are loaded once.
+    // are loaded once, with the first chunk.
     u32x4_t xv[16];
-    {
-        const unsigned char* xb = xs + (lane % bpr) * kXColBytes;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
-    }
+    const unsigned char* xb = xs + (lane % bpr) * kXColBytes;
     for (int i = 0; i < n; ++i) {
         const int slot = i % SLOTS;
         const int issued = min(n, i + SLOTS);
@@ -268,7 +264,21 @@ void gemv_rows_kernel(RowsArgs a) {
         const u32x4_t* pi = reinterpret_cast<const u32x4_t*>(src + 48 * lane);
         const u32x4_t* pc = reinterpret_cast<const u32x4_t*>(src + kSlotIdx + 32 * lane);
         const u32x4_t d0 = pi[0], d1 = pi[1], d2 = pi[2], e0 = pc[0], e1 = pc[1];
-        wait_lds();
+        if (i == 0) {
+            // The activation units go out behind the slot's five reads (the
+            // empty asm keeps the compiler from reordering them). LDS
+            // operations complete in order, so waiting until at most 15 of
+            // the 16 unit reads are outstanding (15: the counter's largest
+            // value) means the slot has been read and may be refilled, while
+            // the dequantization below overlaps the unit reads (the compiler
+            // waits for those before the MFMAs).
+            asm volatile("" : : : "memory");
+#pragma unroll
+            for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
+            asm volatile("s_waitcnt lgkmcnt(15)" : : : "memory");
+        } else {
+            wait_lds();
+        }
         if (i + SLOTS < n) issue(c0 + wave + (i + SLOTS) * kWaves, slot);
         const f32x4_t acc = block_dot(d0, d1, d2, e0, e1, xv);
         dots[(wave + i * kWaves) * 64 + lane] = diag_of(acc, lane);
