@@ -225,6 +225,12 @@ void gemv_rows_kernel(RowsArgs a) {
             for (int w = 0; w < kWaves; ++w) t += rw[w];
             norm = sqrtf(t / (float)K + a.eps);
         }
+        // x / norm for a divisor shared by every element: rn = RN(1 / norm)
+        // by one IEEE division, then q0 = RN(x rn), the exact remainder
+        // x - q0 norm (one fma) and q0 + remainder * rn (one fma), which is
+        // RN(x / norm) (Markstein's correction; values here are far from
+        // overflow and underflow)
+        const float rn = 1.0f / norm;
 #pragma unroll
         for (int j = 0; j < kMaxQ; ++j) {
             const int q = tid + j * kThreads;
@@ -237,8 +243,13 @@ void gemv_rows_kernel(RowsArgs a) {
                 for (int e = 0; e < 4; ++e) {
                     // RMSNorm.forward's (x / norm) * w, generate_torch.py:37; silu(g) * u,
                     // 116-117 (exp(-g) by v_exp_f32, a few ulp, below the bf16 rounding)
-                    const float r = XMODE == NB_X_RMSNORM ? (xv[e] / norm) * sv[e]
-                                                          : (xv[e] / (1.0f + __expf(-xv[e]))) * sv[e];
+                    float r;
+                    if constexpr (XMODE == NB_X_RMSNORM) {
+                        const float q0 = xv[e] * rn;
+                        r = fmaf(fmaf(-q0, norm, xv[e]), rn, q0) * sv[e];
+                    } else {
+                        r = (xv[e] / (1.0f + __expf(-xv[e]))) * sv[e];
+                    }
                     col[staged_half(g & 15, e0 + e)] = f32_to_bf16_rne(r);
                 }
             }
