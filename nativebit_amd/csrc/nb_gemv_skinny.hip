@@ -485,8 +485,8 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     // exist.  Item i's step waits until W(i) and X(i) are in, passes the
     // workgroup barrier (every wave's x pieces of item i are in, and every
     // wave is done with item i - 1, whose x buffer X(i + kLead) refills),
-    // reads slot i into registers, issues its loads -- W(i + kSkDepth)
-    // into the slot just read -- and computes.  kSkDepth slices of weights
+    // reads slot i into registers, issues X(i + kLead), computes, and then
+    // issues W(i + kSkDepth) into the slot it read.  kSkDepth slices of weights
     // are in flight while one is computed.  Loads complete in issue order,
     // so W(i) and X(i) are in once at most after(i) loads are outstanding:
     // those issued after X(i) (the later of the two; kLead <= kSkDepth).
@@ -540,10 +540,6 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             issue_x(cx, (i + kLead) % NXB);
             cursor_next(a, cx, wave);
         }
-        if (i + kSkDepth < nitems) {
-            issue_w(cw, si);
-            cursor_next(a, cw, wave);
-        }
         if (pending) store();
         // ---- compute slice cc.s of the task ----
         const bool live = cc.row0 + r < cc.N && 4 * cc.s + q < cc.bpr;
@@ -564,6 +560,13 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             mfma_units_tile<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
         } else {
             mfma_groups<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+        }
+        // the weights of step i + kSkDepth into the slot read above, after
+        // the MFMAs: issued before them, the five loads can stall at issue
+        // behind a full memory queue, and the wave with them
+        if (i + kSkDepth < nitems) {
+            issue_w(cw, si);
+            cursor_next(a, cw, wave);
         }
         if (cc.s == cc.ns - 1) {
             pend = acc;
