@@ -282,7 +282,10 @@ void gemv_rows_kernel(RowsArgs a) {
             // the 16 unit reads are outstanding (15: the counter's largest
             // value) means the slot has been read and may be refilled, while
             // the dequantization below overlaps the unit reads (the compiler
-            // waits for those before the MFMAs).
+            // waits for those before the MFMAs). This holds while no scalar
+            // memory load is in flight between the slot reads and the wait
+            // (those return out of order on the same counter): the code
+            // between them issues none.
             asm volatile("" : : : "memory");
 #pragma unroll
             for (int j = 0; j < 16; ++j) xv[j] = *reinterpret_cast<const u32x4_t*>(xb + 16 * j);
