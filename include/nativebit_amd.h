@@ -279,6 +279,31 @@ int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
 int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count,
                     int y_dtype, void* stream);
 
+/* The selector-ordered unit layout of a 3-bit stream: the same bytes, each
+ * 12-byte unit of 32 indices rewritten so that the batched kernels take
+ * its eight four-index selectors with one shift and one mask each (17 VALU
+ * ops per 32 indices instead of 25).  With o = (0, 1, 3, 4, 6, 7, 2, 5),
+ * byte k (0..3) of the unit's dword 0 holds index o(0)+8k in bits 0-2,
+ * o(1)+8k in bits 3-5 and the low two bits of o(6)+8k in bits 6-7;
+ * dword 1 likewise o(2)+8k, o(3)+8k and the low bits of o(7)+8k; dword 2
+ * o(4)+8k, o(5)+8k, the high bit of o(6)+8k (bit 6) and of o(7)+8k
+ * (bit 7).  Writes the N*K*3/8 bytes of `out` (out == packed allowed);
+ * K a multiple of 128, both pointers 4-byte aligned.  The codebook is
+ * unchanged.
+ * No counterpart in the reference: a one-time re-ordering of a layer's
+ * stream (for instance at model load) for nb_gemv_batched_sel. */
+int nb_stream_layout(const uint8_t* packed, uint8_t* out, int N, int K, void* stream);
+
+/* nb_gemv_batched on streams in the selector-ordered unit layout: every
+ * item's packed is nb_stream_layout's output for that item's N x K, all
+ * else as for nb_gemv_batched (same table, same fused forms).  The same
+ * products, bit for bit, with less dequantization work per weight.
+ * Replaces the same reference paths as nb_gemv_batched
+ * (inference/cuda_kernel.py:38-104, inference/triton_kernel.py:143-196,
+ * bf16 form of inference/eval_ppl.py:149-174) for layers converted once. */
+int nb_gemv_batched_sel(const nb_batch_item* items, const void* table_dev, int count,
+                        int y_dtype, void* stream);
+
 /* Batched skinny GEMM: the same batch with M (1..16) activation rows per
  * item -- the batched branch of PackedLinear.forward (inference/
  * triton_kernel.py:258-275) in its bf16 form (inference/eval_ppl.py:149-174)

@@ -61,6 +61,8 @@ SIGNATURES = {
     "nb_gemv_batch_table_bytes": (_L, [_I]),
     "nb_gemv_batch_plan": (_I, [_P, _I, _P, _L]),
     "nb_gemv_batched": (_I, [_P, _P, _I, _I, _P]),
+    "nb_gemv_batched_sel": (_I, [_P, _P, _I, _I, _P]),
+    "nb_stream_layout": (_I, [_P, _P, _I, _I, _P]),
     "nb_gemm_skinny_batched": (_I, [_P, _P, _I, _I, _I, _P]),
     "nb_quad_layout_bytes": (_L, [_I, _I]),
     "nb_quad_layout": (_I, [_P, _P, _I, _I, _P, _P, _P]),

@@ -371,32 +371,10 @@ int check_batch(const nb_batch_item* items, int count, const char* fn, int64_t* 
     return NB_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
-                       int64_t table_bytes) {
-    const char* fn = "nb_gemv_batch_plan";
-    int64_t chunks = 0;
-    int mk = 0;
-    int st = check_batch(items, count, fn, &chunks, &mk);
-    if (st) return st;
-    if (table_bytes < nb_gemv_batch_table_bytes(count)) {
-        return fail(NB_EINVAL, "%s: table of %lld bytes, %lld needed", fn, (long long)table_bytes,
-                    (long long)nb_gemv_batch_table_bytes(count));
-    }
-    if (count > 0 && !table_host) return fail(NB_EINVAL, "%s: table_host is NULL", fn);
-    // Items with N == 0 are left out; the table holds the others in order and
-    // the unused tail of the table is zeroed.
-    memset(table_host, 0, (size_t)nb_gemv_batch_table_bytes(count));
-    build_stream_table(items, count, static_cast<StreamProblem*>(table_host));
-    return NB_OK;
-}
-
-int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count, int y_dtype,
-                    void* stream) {
-    const char* fn = "nb_gemv_batched";
+// nb_gemv_batched and nb_gemv_batched_sel: the same checks and kernels; sel
+// says the index streams are in the selector-ordered unit layout.
+int gemv_batched(const char* fn, const nb_batch_item* items, const void* table_dev, int count,
+                 int y_dtype, bool sel, void* stream) {
     int64_t chunks = 0;
     int mk = 0;
     int st = check_batch(items, count, fn, &chunks, &mk);
@@ -429,7 +407,55 @@ int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count
                     "kernel's LDS", fn);
     }
     return launch_gemv_stream(static_cast<const StreamProblem*>(table_dev), host.data(), nprob,
-                              y_dtype, static_cast<hipStream_t>(stream));
+                              y_dtype, sel, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int nb_gemv_batch_plan(const nb_batch_item* items, int count, void* table_host,
+                       int64_t table_bytes) {
+    const char* fn = "nb_gemv_batch_plan";
+    int64_t chunks = 0;
+    int mk = 0;
+    int st = check_batch(items, count, fn, &chunks, &mk);
+    if (st) return st;
+    if (table_bytes < nb_gemv_batch_table_bytes(count)) {
+        return fail(NB_EINVAL, "%s: table of %lld bytes, %lld needed", fn, (long long)table_bytes,
+                    (long long)nb_gemv_batch_table_bytes(count));
+    }
+    if (count > 0 && !table_host) return fail(NB_EINVAL, "%s: table_host is NULL", fn);
+    // Items with N == 0 are left out; the table holds the others in order and
+    // the unused tail of the table is zeroed.
+    memset(table_host, 0, (size_t)nb_gemv_batch_table_bytes(count));
+    build_stream_table(items, count, static_cast<StreamProblem*>(table_host));
+    return NB_OK;
+}
+
+int nb_gemv_batched(const nb_batch_item* items, const void* table_dev, int count, int y_dtype,
+                    void* stream) {
+    return gemv_batched("nb_gemv_batched", items, table_dev, count, y_dtype, false, stream);
+}
+
+int nb_gemv_batched_sel(const nb_batch_item* items, const void* table_dev, int count,
+                        int y_dtype, void* stream) {
+    return gemv_batched("nb_gemv_batched_sel", items, table_dev, count, y_dtype, true, stream);
+}
+
+int nb_stream_layout(const uint8_t* packed, uint8_t* out, int N, int K, void* stream) {
+    const char* fn = "nb_stream_layout";
+    if (N < 0) return fail(NB_EINVAL, "%s: N=%d", fn, N);
+    if (K <= 0 || K % 128) return fail(NB_EINVAL, "%s: K=%d must be a positive multiple of 128", fn, K);
+    if (N == 0) return NB_OK;
+    if (!packed || !out) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (!aligned(packed, 4) || !aligned(out, 4)) {
+        return fail(NB_EALIGN, "%s: packed/out not 4-byte aligned", fn);
+    }
+    const int st = ensure_device();
+    if (st) return st;
+    return launch_stream_layout(packed, out, (int64_t)N * (K / 32),
+                                static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -99,7 +99,9 @@ __device__ __forceinline__ void dma_piece(uint32_t lds, const uint8_t* base, int
     dma16<0>(__builtin_amdgcn_readfirstlane(lds + p * 1024), src < last ? src : last);
 }
 
-template <int XMODE, int SLOTS>
+// kSel: the index stream is in the selector-ordered unit layout
+// (nb_stream_layout); the products are the same.
+template <int XMODE, int SLOTS, bool kSel>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3)))
 void gemv_rows_kernel(RowsArgs a) {
     extern __shared__ __align__(16) unsigned char smem[];
@@ -294,7 +296,7 @@ void gemv_rows_kernel(RowsArgs a) {
             wait_lds();
         }
         if (i + SLOTS < n) issue(c0 + wave + (i + SLOTS) * kWaves, slot);
-        const f32x4_t acc = block_dot(d0, d1, d2, e0, e1, xv);
+        const f32x4_t acc = block_dot<kSel>(d0, d1, d2, e0, e1, xv);
         dots[(wave + i * kWaves) * 64 + lane] = diag_of(acc, lane);
     }
     __syncthreads();
@@ -372,14 +374,23 @@ RowsShape rows_shape(const StreamProblem& p) {
     return s;
 }
 
-template <int XMODE>
+template <int XMODE, bool kSel>
 void launch_mode(const RowsShape& s, const RowsArgs& a, hipStream_t stream) {
     if (s.slots == 3) {
-        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 3>), dim3(s.G), dim3(kThreads), s.lds,
+        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 3, kSel>), dim3(s.G), dim3(kThreads), s.lds,
                            stream, a);
     } else {
-        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 2>), dim3(s.G), dim3(kThreads), s.lds,
+        hipLaunchKernelGGL((gemv_rows_kernel<XMODE, 2, kSel>), dim3(s.G), dim3(kThreads), s.lds,
                            stream, a);
+    }
+}
+
+template <bool kSel>
+void launch_modes(int x_mode, const RowsShape& s, const RowsArgs& a, hipStream_t stream) {
+    switch (x_mode) {
+        case NB_X_BF16: launch_mode<NB_X_BF16, kSel>(s, a, stream); break;
+        case NB_X_RMSNORM: launch_mode<NB_X_RMSNORM, kSel>(s, a, stream); break;
+        default: launch_mode<NB_X_SILU_MUL, kSel>(s, a, stream); break;
     }
 }
 
@@ -390,7 +401,7 @@ bool gemv_rows_fits(const StreamProblem& p) {
     return rows_shape(p).lds <= (size_t)device_lds_bytes();
 }
 
-int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream) {
+int launch_gemv_rows(const StreamProblem& p, int y_dtype, bool sel, hipStream_t stream) {
     const RowsShape s = rows_shape(p);
     RowsArgs a;
     a.packed = p.packed;
@@ -409,10 +420,10 @@ int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream) {
     a.y_mode = p.y_mode;
     a.y_dtype = y_dtype;
     a.eps = p.eps;
-    switch (p.x_mode) {
-        case NB_X_BF16: launch_mode<NB_X_BF16>(s, a, stream); break;
-        case NB_X_RMSNORM: launch_mode<NB_X_RMSNORM>(s, a, stream); break;
-        default: launch_mode<NB_X_SILU_MUL>(s, a, stream); break;
+    if (sel) {
+        launch_modes<true>(p.x_mode, s, a, stream);
+    } else {
+        launch_modes<false>(p.x_mode, s, a, stream);
     }
     return check_launch("nb_gemv_batched");
 }

@@ -228,6 +228,9 @@ __device__ __forceinline__ void stage_problem(const ProbL* sp, unsigned char* co
     }
 }
 
+// kSel: every problem's index stream is in the selector-ordered unit layout
+// (nb_stream_layout); the products are the same.
+template <bool kSel>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kWaves / 4, kWaves / 4)))
 void gemv_stream_kernel(
     const StreamProblem* __restrict__ probs, StreamRanges ranges, int y_dtype) {
@@ -418,7 +421,7 @@ void gemv_stream_kernel(
         auto compute = [&](const SlotRegs& r, const Meta& m, const Lane& L,
                            const u32x4_t (&xv)[16]) {
             // a block that is not live computes garbage on its own diagonal only
-            const f32x4_t a = block_dot(r.d0, r.d1, r.d2, r.c0, r.c1, xv);
+            const f32x4_t a = block_dot<kSel>(r.d0, r.d1, r.d2, r.c0, r.c1, xv);
             const int l3 = lane & 3;
             const float dot = l3 == 0 ? a.x : l3 == 1 ? a.y : l3 == 2 ? a.z : a.w;
             // quad pre-sum where the quad's four blocks share a row
@@ -553,12 +556,43 @@ static int aligned_at(const StreamProblem* hp, int nprob, int64_t c) {
     return P.chunk_begin + (int)up;
 }
 
+namespace {
+
+// nb_stream_layout: one thread per 12-byte unit; the unit's eight selectors
+// (unit_selectors) packed back as the selector-ordered unit (sel_unit_pack).
+// A thread reads its unit before writing it, so in == out is allowed.
+__global__ __launch_bounds__(256) void stream_layout_kernel(const uint32_t* in, uint32_t* out,
+                                                            int64_t units) {
+    for (int64_t u = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; u < units;
+         u += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t d0 = in[3 * u], d1 = in[3 * u + 1], d2 = in[3 * u + 2];
+        uint32_t sel[8];
+        unit_selectors(d0, d1, d2, sel);
+        uint32_t e0, e1, e2;
+        sel_unit_pack(sel, e0, e1, e2);
+        out[3 * u] = e0;
+        out[3 * u + 1] = e1;
+        out[3 * u + 2] = e2;
+    }
+}
+
+}  // namespace
+
+int launch_stream_layout(const uint8_t* in, uint8_t* out, int64_t units, hipStream_t stream) {
+    if (units == 0) return NB_OK;
+    const int64_t grid = std::min<int64_t>((units + 255) / 256, (int64_t)device_cu_count() * 8);
+    hipLaunchKernelGGL(stream_layout_kernel, dim3((int)grid), dim3(256), 0, stream,
+                       reinterpret_cast<const uint32_t*>(in), reinterpret_cast<uint32_t*>(out),
+                       units);
+    return check_launch("nb_stream_layout");
+}
+
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
-                       int nprob, int y_dtype, hipStream_t stream) {
+                       int nprob, int y_dtype, bool sel, hipStream_t stream) {
     if (nprob == 0) return NB_OK;
     // a single problem (a decode step's launch) takes the whole-row kernel
     if (nprob == 1 && gemv_rows_fits(host_probs[0])) {
-        return launch_gemv_rows(host_probs[0], y_dtype, stream);
+        return launch_gemv_rows(host_probs[0], y_dtype, sel, stream);
     }
     const StreamProblem& last = host_probs[nprob - 1];
     const int total = last.chunk_begin + last.nchunks;
@@ -620,8 +654,13 @@ int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host
             lds = std::max(lds, range_lds(host_probs, R.prob0[i], R.prob1[i], R.chunk0[i],
                                           R.chunk0[i + 1]));
         }
-        hipLaunchKernelGGL(gemv_stream_kernel, dim3(n), dim3(64 * kWaves), (size_t)lds, stream,
-                           dev_probs, R, y_dtype);
+        if (sel) {
+            hipLaunchKernelGGL(gemv_stream_kernel<true>, dim3(n), dim3(64 * kWaves), (size_t)lds,
+                               stream, dev_probs, R, y_dtype);
+        } else {
+            hipLaunchKernelGGL(gemv_stream_kernel<false>, dim3(n), dim3(64 * kWaves), (size_t)lds,
+                               stream, dev_probs, R, y_dtype);
+        }
         const int st = check_launch("nb_gemv_batched");
         if (st) return st;
     }

@@ -88,9 +88,14 @@ int build_stream_table(const nb_batch_item* items, int count, StreamProblem* out
 // One problem per launch, whole-row chunks (nb_gemv_rows.hip): the launches
 // of a decode step.  gemv_rows_fits says whether its LDS holds the problem.
 bool gemv_rows_fits(const StreamProblem& p);
-int launch_gemv_rows(const StreamProblem& p, int y_dtype, hipStream_t stream);
+// sel: the index streams are in the selector-ordered unit layout
+// (launch_stream_layout).
+int launch_gemv_rows(const StreamProblem& p, int y_dtype, bool sel, hipStream_t stream);
 int launch_gemv_stream(const StreamProblem* dev_probs, const StreamProblem* host_probs,
-                       int nprob, int y_dtype, hipStream_t stream);
+                       int nprob, int y_dtype, bool sel, hipStream_t stream);
+// Rewrites `units` 12-byte units of a 3-bit stream into the selector-ordered
+// unit layout (in place allowed).
+int launch_stream_layout(const uint8_t* in, uint8_t* out, int64_t units, hipStream_t stream);
 
 // Launches the batched skinny GEMM (M <= 16 activation rows) over the
 // problem table.

@@ -83,6 +83,37 @@ __device__ __forceinline__ void unit_selectors(uint32_t d0, uint32_t d1, uint32_
     sel[7] = ((u >> 7) & 0x01010101u) | ((e << 1) & 0x06060606u);
 }
 
+// The selector-ordered unit (nb_stream_layout, made once at load): the same
+// 32 indices and 96 bits, placed so that selector s holds the same four
+// indices as above.  Byte k of dword 0 holds index o(0)+8k in bits 0-2,
+// o(1)+8k in bits 3-5 and the low two bits of o(6)+8k in bits 6-7; dword 1
+// likewise o(2)+8k, o(3)+8k and the low bits of o(7)+8k; dword 2 o(4)+8k,
+// o(5)+8k and the high bits of o(6)+8k (bit 6) and o(7)+8k (bit 7).  Six
+// selectors are then one shift and one mask each, the last two two
+// shifts, two masks and an or: 17 VALU ops for 32 indices.
+__device__ __forceinline__ void unit_selectors_sel(uint32_t d0, uint32_t d1, uint32_t d2,
+                                                   uint32_t (&sel)[8]) {
+    const uint32_t M = 0x07070707u;
+    sel[0] = d0 & M;
+    sel[1] = (d0 >> 3) & M;
+    sel[2] = d1 & M;
+    sel[3] = (d1 >> 3) & M;
+    sel[4] = d2 & M;
+    sel[5] = (d2 >> 3) & M;
+    sel[6] = ((d0 >> 6) & 0x03030303u) | ((d2 >> 4) & 0x04040404u);
+    sel[7] = ((d1 >> 6) & 0x03030303u) | ((d2 >> 5) & 0x04040404u);
+}
+
+// The selector-ordered unit of the eight selectors of a unit (the inverse of
+// unit_selectors_sel for selectors whose bytes are 0..7).
+__host__ __device__ __forceinline__ void sel_unit_pack(const uint32_t (&sel)[8], uint32_t& d0,
+                                                      uint32_t& d1, uint32_t& d2) {
+    d0 = sel[0] | (sel[1] << 3) | ((sel[6] & 0x03030303u) << 6);
+    d1 = sel[2] | (sel[3] << 3) | ((sel[7] & 0x03030303u) << 6);
+    d2 = sel[4] | (sel[5] << 3) | (((sel[6] >> 2) & 0x01010101u) << 6) |
+         (((sel[7] >> 2) & 0x01010101u) << 7);
+}
+
 __device__ __forceinline__ f32x4_t mfma44(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1,
                                           f32x4_t c) {
     u32x2_t a = {a0, a1}, b = {b0, b1};
@@ -165,8 +196,11 @@ __device__ __forceinline__ void stage_unit(unsigned char* col, int u, const uint
 // The lane's dot product of its block (index dwords rd0..rd2, codebook
 // rc0..rc1) with the staged activations of its column (xv = the column
 // block's 16 units), as the four accumulators whose element (lane & 3)
-// holds it (see diag_of).  The block's registers are taken by value: a
-// reference to a caller's struct made the register allocator spill them.
+// holds it (see diag_of).  kSel: the index bytes are in the
+// selector-ordered unit layout (same selectors, same products).  The
+// block's registers are taken by value: a reference to a caller's struct
+// made the register allocator spill them.
+template <bool kSel = false>
 __device__ __forceinline__ f32x4_t block_dot(u32x4_t rd0, u32x4_t rd1, u32x4_t rd2, u32x4_t rc0,
                                              u32x4_t rc1, const u32x4_t (&xv)[16]) {
     const SlotRegs r = {rd0, rd1, rd2, rc0, rc1};
@@ -185,7 +219,11 @@ __device__ __forceinline__ f32x4_t block_dot(u32x4_t rd0, u32x4_t rd1, u32x4_t r
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
         uint32_t sel[8];
-        unit_selectors(d[3 * u], d[3 * u + 1], d[3 * u + 2], sel);
+        if constexpr (kSel) {
+            unit_selectors_sel(d[3 * u], d[3 * u + 1], d[3 * u + 2], sel);
+        } else {
+            unit_selectors(d[3 * u], d[3 * u + 1], d[3 * u + 2], sel);
+        }
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sel[s]);

@@ -162,7 +162,10 @@ class GemvBatch:
     are the row-quad layout of its layer (``quad_layout``), run by
     nb_gemm_skinny_quad_batched.  ``layout="tile"`` (m > 1): every item's
     packed / codebook are the tile layout of its layer (``tile_layout``),
-    run by nb_gemm_skinny_tile_batched.
+    run by nb_gemm_skinny_tile_batched.  ``layout="sel"`` (m == 1): every
+    item's packed is the selector-ordered unit layout of its stream
+    (``stream_layout``; codebook unchanged), run by nb_gemv_batched_sel with
+    every activation and output form.
 
     The device table is built once here; each run() enqueues one launch on
     torch's current stream (graph-capturable).  The tensors are referenced
@@ -172,8 +175,10 @@ class GemvBatch:
     def __init__(self, items, m: int = 1, layout: str = "rows"):
         if not 1 <= m <= 16:
             raise ValueError(f"m={m} outside 1..16")
-        if layout not in ("rows", "quad", "tile"):
+        if layout not in ("rows", "quad", "tile", "sel"):
             raise ValueError(f"unknown layout {layout!r}")
+        if layout == "sel" and m != 1:
+            raise ValueError("the selector-ordered layout is for m == 1 (nb_gemv_batched_sel)")
         if layout == "quad" and m > 4:
             raise ValueError(f"the row-quad kernel takes m <= 4 (got {m})")
         if layout == "tile" and m < 2:
@@ -268,6 +273,9 @@ class GemvBatch:
             _lib.check(lib.nb_gemm_skinny_tile_batched(self._arr, self.table.data_ptr(),
                                                        self.count, self.m, _DT[self.y_dtype],
                                                        stream))
+        elif self.layout == "sel":
+            _lib.check(lib.nb_gemv_batched_sel(self._arr, self.table.data_ptr(), self.count,
+                                               _DT[self.y_dtype], stream))
         elif self.m == 1:
             _lib.check(lib.nb_gemv_batched(self._arr, self.table.data_ptr(), self.count,
                                            _DT[self.y_dtype], stream))
@@ -325,6 +333,32 @@ def tile_layout(packed: torch.Tensor, codebook: torch.Tensor, N: int, K: int):
     _lib.check(lib.nb_tile_layout(packed.data_ptr(), codebook.data_ptr(), N, K, tp.data_ptr(),
                                   tc.data_ptr(), _stream(packed)))
     return tp, tc
+
+
+def stream_layout(packed: torch.Tensor, N: int, K: int, out: torch.Tensor | None = None):
+    """The selector-ordered unit layout of the 3-bit stream of an N x K layer
+    (nb_stream_layout): the same N*K*3/8 bytes, each 12-byte unit's bits
+    placed so that the batched kernels take its selectors with one shift and
+    one mask each.  The codebook is unchanged.  Returns the new uint8 stream
+    (``out`` if given; ``out`` may be ``packed`` itself), for
+    GemvBatch(..., layout="sel")."""
+    _require_cuda("packed", packed)
+    if packed.dtype != torch.uint8 or not packed.is_contiguous():
+        raise TypeError("packed must be a contiguous uint8 tensor")
+    if N < 0 or K <= 0 or K % 128:
+        raise ValueError(f"N={N}, K={K}: K must be a positive multiple of 128")
+    nbytes = N * K * 3 // 8
+    if packed.numel() < nbytes:
+        raise ValueError(f"packed has {packed.numel()} bytes, {nbytes} needed")
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=packed.device)
+    elif (out.dtype != torch.uint8 or not out.is_contiguous() or out.numel() < nbytes or
+          out.device != packed.device):
+        raise ValueError(f"out must be a contiguous uint8 tensor of >= {nbytes} bytes on "
+                         f"{packed.device}")
+    lib = _lib.load()
+    _lib.check(lib.nb_stream_layout(packed.data_ptr(), out.data_ptr(), N, K, _stream(packed)))
+    return out
 
 
 def gemm_prefill(x: torch.Tensor, packed: torch.Tensor, codebook: torch.Tensor, N: int,
