@@ -190,10 +190,13 @@ class DecodeEngine(_DecoderBase):
     _gu_rows = "interleaved"   # the gate|up GEMV hands silu(gate) * up to down
 
     def __init__(self, model: PackedGPT, max_steps: int | None = None,
-                 record_layers: bool = False):
+                 record_layers: bool = False, sel_layout: bool = True):
         """``record_layers``: after every layer the step also copies the
         residual stream into ``self.layer_x[l]`` (for layer-by-layer
-        comparisons; one extra copy launch per layer)."""
+        comparisons; one extra copy launch per layer).  ``sel_layout``: the
+        step's GEMVs read copies of the index streams re-ordered into the
+        selector-ordered unit layout (nb_stream_layout; less dequantization
+        work, bit-identical outputs); the prompt pass keeps the originals."""
         super().__init__(model, max_steps)
         C, F, H = self.C, self.F, self.H
         self.layer_x = self._z(model.cfg.n_layers, C) if record_layers else None
@@ -212,16 +215,22 @@ class DecodeEngine(_DecoderBase):
         eps = self.eps
         add = {"y": "add"}
         self.gemvs = []
+        lay = "sel" if sel_layout else "rows"
         for l, ((qkv_p, qkv_c), (o_p, o_c), (gu_p, gu_c), (d_p, d_c)) in enumerate(self.fused):
             ln1, ln2 = self.norms[l]
+            if sel_layout:
+                qkv_p = ops.stream_layout(qkv_p, 3 * C, C)
+                o_p = ops.stream_layout(o_p, C, C)
+                gu_p = ops.stream_layout(gu_p, 2 * F, C)
+                d_p = ops.stream_layout(d_p, C, F)
             qkv_item = ((self.h, qkv_p, qkv_c, self.qkv, 3 * C, C) if l == 0 else
                         (self.x, qkv_p, qkv_c, self.qkv, 3 * C, C, {"x": ("rmsnorm", ln1, eps)}))
             self.gemvs.append((
-                ops.GemvBatch([qkv_item]),
-                ops.GemvBatch([(self.att, o_p, o_c, self.x, C, C, add)]),
+                ops.GemvBatch([qkv_item], layout=lay),
+                ops.GemvBatch([(self.att, o_p, o_c, self.x, C, C, add)], layout=lay),
                 ops.GemvBatch([(self.x, gu_p, gu_c, self.act, 2 * F, C,
-                                {"x": ("rmsnorm", ln2, eps), "y": "silu_pairs"})]),
-                ops.GemvBatch([(self.act, d_p, d_c, self.x, C, F, add)]),
+                                {"x": ("rmsnorm", ln2, eps), "y": "silu_pairs"})], layout=lay),
+                ops.GemvBatch([(self.act, d_p, d_c, self.x, C, F, add)], layout=lay),
             ))
         self.graph = None
         self._prompt_graphs = {}   # prompt length -> (graph, buffers) of the prompt pass
