@@ -377,6 +377,7 @@ void gemv_stream_kernel(
         // Per-chunk lane state computed before the chunk's bytes arrive.
         struct Lane {
             int row;
+            int col;  // the block's column block in its row
             bool live;
         };
         // The lane's block, row and column; requests its 16 activation
@@ -396,6 +397,7 @@ void gemv_stream_kernel(
             row += rem >= CP.bpr ? 1 : (rem < 0 ? -1 : 0);
             rem = beta - (int)__umul24((unsigned)row, (unsigned)CP.bpr);
             L.row = row;
+            L.col = rem;
             const int col = L.live ? rem : 0;
             const unsigned char* xb = xregion + CP.x_off + col * kXColBytes;
 #pragma unroll
@@ -432,9 +434,11 @@ void gemv_stream_kernel(
             const float s4 = s2 + quad_mov<quad_perm(2, 3, 0, 1)>(s2);
             if (L.live && (!quad_row || l3 == 0)) {
                 // a row that began in the previous chunk goes to this
-                // chunk's carry slot
-                const bool carry = L.row * CP.bpr < m.lc * kChunkBlocks;
-                const int slot = carry ? CP.carry_off + m.lc - CP.ca : CP.y_off + L.row - CP.row_a;
+                // chunk's carry slot: its first block is lane - col < 0 of
+                // this chunk (the chunk starts at block lc * 64)
+                const int cbase = __builtin_amdgcn_readfirstlane(CP.carry_off + m.lc - CP.ca);
+                const int ybase = __builtin_amdgcn_readfirstlane(CP.y_off - CP.row_a);
+                const int slot = L.col > lane ? cbase : ybase + L.row;
                 atomicAdd(ybuf + slot, quad_row ? s4 : dot);
             }
         };
