@@ -319,8 +319,9 @@ int nb_gemm_skinny_batched(const nb_batch_item* items, const void* table_dev, in
  * 128-weight blocks (48 index bytes, 8 fp32 codebook entries each) with the
  * rows taken four at a time (N rounded up to a multiple of 4 with zero
  * blocks) and the four rows' blocks of one column block side by side:
- *     block 4 (q * K/128 + kb) + i  =  row 4q + i, column block kb.
- * qpacked holds nb_quad_layout_bytes(N, K) bytes, qcodebook
+ *     block 4 (q * K/128 + kb) + i  =  row 4q + i, column block kb,
+ * each 12-byte unit of a block's indices in the selector-ordered unit
+ * layout of nb_stream_layout.  qpacked holds nb_quad_layout_bytes(N, K) bytes, qcodebook
  * nb_quad_layout_bytes(N, K) * 2 / 3 bytes (ceil(N/4) * 4 * K/128 * 8
  * floats); both 16-byte aligned, as packed and codebook.
  * No counterpart in the reference: a one-time re-ordering of a layer's
@@ -349,9 +350,9 @@ int nb_gemm_skinny_quad_batched(const nb_batch_item* items, const void* table_de
  * holds them: row r's 48-byte blocks b at block place
  * (b + ((r >> 1) & 3) + (r >> 3)) & 3 of its 192 bytes, its codebook
  * 16-byte pieces p at place (p + ((r & 6) | ((r ^ (r >> 3)) & 1))) & 7 of
- * its 128 bytes, and within every 12-byte unit of 32 indices index 4s + t
- * (s = 0..7, t = 0..3) at index position o(s) + 8t,
- * o = (0, 1, 3, 4, 6, 7, 2, 5).  tpacked holds nb_tile_layout_bytes(N, K)
+ * its 128 bytes, and every 12-byte unit of 32 indices in the
+ * selector-ordered unit layout of nb_stream_layout with selector s (s =
+ * 0..7) holding indices 4s .. 4s + 3 (byte t: index 4s + t).  tpacked holds nb_tile_layout_bytes(N, K)
  * bytes, tcodebook nb_tile_layout_bytes(N, K) * 2 / 3 bytes; all four
  * pointers 16-byte aligned.
  * No counterpart in the reference: a one-time re-ordering of a layer (for

@@ -351,7 +351,7 @@ void gemv_quad_kernel(QuadArgs a) {
         store_pending();
         const int c = m.c;
         issue(slot, m);
-        const f32x4_t d = block_dot(d0, d1, d2, e0, e1, xv);
+        const f32x4_t d = block_dot<true>(d0, d1, d2, e0, e1, xv);
         // lane 4g+j, accumulator i: row 4q+i, token j.  acc holds the lane's
         // sums for the quad of its latest pair; a lane's pair moves to the
         // next quad at most once a chunk (bpr >= 16), in the chunk where
@@ -527,22 +527,44 @@ __global__ __launch_bounds__(256) void quad_layout_kernel(const uint8_t* __restr
                                                           int N, int bpr, int64_t nblocks,
                                                           uint8_t* __restrict__ qpacked,
                                                           float* __restrict__ qcodebook) {
+    // three threads a block: its 48 index bytes (four 12-byte units, each
+    // rewritten as the selector-ordered unit) and the two halves of its
+    // eight codebook entries
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= nblocks * 5) return;
-    const int64_t b = t / 5;
-    const int piece = (int)(t - b * 5);
+    if (t >= nblocks * 3) return;
+    const int64_t b = t / 3;
+    const int piece = (int)(t - b * 3);
     const int64_t pr = b >> 2;
     const int i = (int)(b & 3);
     const int64_t q = pr / bpr;
     const int kb = (int)(pr - q * bpr);
     const int64_t row = 4 * q + i;
     typedef __attribute__((ext_vector_type(4))) uint32_t v4;
-    v4 v = {0u, 0u, 0u, 0u};
-    if (piece < 3) {
-        if (row < N) v = *reinterpret_cast<const v4*>(packed + (row * bpr + kb) * 48 + 16 * piece);
-        *reinterpret_cast<v4*>(qpacked + b * 48 + 16 * piece) = v;
+    if (piece == 0) {
+        uint32_t w[12] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+        if (row < N) {
+            const v4* src = reinterpret_cast<const v4*>(packed + (row * bpr + kb) * 48);
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const v4 v = src[j];
+                w[4 * j] = v.x;
+                w[4 * j + 1] = v.y;
+                w[4 * j + 2] = v.z;
+                w[4 * j + 3] = v.w;
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            uint32_t sel[8];
+            unit_selectors(w[3 * u], w[3 * u + 1], w[3 * u + 2], sel);
+            sel_unit_pack(sel, w[3 * u], w[3 * u + 1], w[3 * u + 2]);
+        }
+        v4* dst = reinterpret_cast<v4*>(qpacked + b * 48);
+#pragma unroll
+        for (int j = 0; j < 3; ++j) dst[j] = v4{w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
     } else {
-        const int h = piece - 3;
+        const int h = piece - 1;
+        v4 v = {0u, 0u, 0u, 0u};
         if (row < N) v = *reinterpret_cast<const v4*>(codebook + (row * bpr + kb) * 8 + 4 * h);
         *reinterpret_cast<v4*>(qcodebook + b * 8 + 4 * h) = v;
     }
@@ -554,7 +576,7 @@ int launch_quad_layout(const uint8_t* packed, const float* codebook, int N, int 
                        uint8_t* qpacked, float* qcodebook, hipStream_t stream) {
     const int bpr = K / 128;
     const int64_t nblocks = (int64_t)((N + 3) / 4) * 4 * bpr;
-    const int64_t threads = nblocks * 5;
+    const int64_t threads = nblocks * 3;
     if (threads == 0) return NB_OK;
     hipLaunchKernelGGL(quad_layout_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        stream, packed, codebook, N, bpr, nblocks, qpacked, qcodebook);

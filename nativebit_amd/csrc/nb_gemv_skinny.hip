@@ -170,8 +170,9 @@ __device__ __forceinline__ void mfma_groups(const uint32_t (&d)[12], uint32_t lo
 }
 
 // The same 16 MFMAs on the tile layout's index order: unit U (32 indices,
-// dwords d[3U .. 3U + 2]) gives groups 4U .. 4U + 3, selectors 2p and
-// 2p + 1 being the eight weights of group 4U + p in natural order.
+// dwords d[3U .. 3U + 2], a selector-ordered unit) gives groups 4U .. 4U +
+// 3, selectors 2p and 2p + 1 being the eight weights of group 4U + p in
+// natural order (17 VALU ops a unit to take the selectors).
 template <int U>
 __device__ __forceinline__ void mfma_units_tile(const uint32_t (&d)[12], uint32_t lo0,
                                                uint32_t lo1, uint32_t hi0, uint32_t hi1,
@@ -179,7 +180,7 @@ __device__ __forceinline__ void mfma_units_tile(const uint32_t (&d)[12], uint32_
                                                f32x4_t& acc) {
     if constexpr (U < 4) {
         uint32_t sel[8];
-        stream::unit_selectors(d[3 * U], d[3 * U + 1], d[3 * U + 2], sel);
+        stream::unit_selectors_sel(d[3 * U], d[3 * U + 1], d[3 * U + 2], sel);
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
             const uint32_t la = __builtin_amdgcn_perm(lo1, lo0, sel[2 * p]);
@@ -614,7 +615,8 @@ __device__ __forceinline__ void sel_unit(const uint32_t* in, uint32_t* out) {
 }
 
 // One thread per block place of a tile (64 per tile: row rr, block blk of
-// the slice): the block's 48 index bytes in selector order at the rotated
+// the slice): the block's 48 index bytes (each 12-byte unit the
+// selector-ordered unit whose selector s holds indices 4s .. 4s + 3) at the rotated
 // place the kernel's slot holds them, its 8 codebook entries as two
 // rotated 16-byte pieces; zeros where the row or block is past the layer.
 __global__ __launch_bounds__(256) void tile_layout_kernel(const uint8_t* packed,
@@ -642,7 +644,14 @@ __global__ __launch_bounds__(256) void tile_layout_kernel(const uint8_t* packed,
             d[4 * v + 3] = u.w;
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) sel_unit<0>(d + 3 * u, o + 3 * u);
+        for (int u = 0; u < 4; ++u) {
+            // selector s = indices 4s .. 4s + 3, stored as the
+            // selector-ordered unit (nb_stream_common.h, sel_unit_pack)
+            uint32_t so[3] = {0u, 0u, 0u}, sel[8];
+            sel_unit<0>(d + 3 * u, so);
+            stream::unit_selectors(so[0], so[1], so[2], sel);
+            stream::sel_unit_pack(sel, o[3 * u], o[3 * u + 1], o[3 * u + 2]);
+        }
         const u32x4_t* cs = reinterpret_cast<const u32x4_t*>(codebook + b * 8);
         c0 = cs[0];
         c1 = cs[1];

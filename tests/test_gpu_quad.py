@@ -2,7 +2,8 @@
 skinny kernel on it (nb_gemm_skinny_quad_batched), run with -m gpu.
 
 Bars: the layout is byte-exact against a numpy re-ordering of the
-reference layout's blocks; the products are within 1e-3 (relative L2) of
+reference layout's blocks with every 12-byte unit in the selector-ordered
+unit layout (tests/test_stream_layout.py); the products are within 1e-3 (relative L2) of
 the fp64 brute force on the bf16-rounded weights (the reference's bf16
 path, inference/eval_ppl.py:149-174), deterministic, and a bf16 output is
 the RNE rounding of the fp32 one."""
@@ -12,14 +13,17 @@ import torch
 
 from nativebit_amd import ops
 
+from oracle import oracle as O
 from test_gpu_parity import REL_F32, note, random_layer, ref_gemv, rel
+from test_stream_layout import sel_layout_np
 
 pytestmark = pytest.mark.gpu
 
 
 def quad_order_np(p, cb, N, K):
     """The row-quad layout by array re-shaping: blocks [N, bpr] -> rows
-    padded to a multiple of 4 with zero blocks -> [nq, 4, bpr] -> [nq, bpr, 4]."""
+    padded to a multiple of 4 with zero blocks -> [nq, 4, bpr] -> [nq, bpr, 4],
+    then every 12-byte unit in the selector-ordered unit layout."""
     bpr = K // 128
     nq = -(-N // 4)
     ib = np.zeros((nq * 4, bpr, 48), np.uint8)
@@ -28,7 +32,7 @@ def quad_order_np(p, cb, N, K):
     c[:N] = cb.reshape(N, bpr, 8)
     ib = ib.reshape(nq, 4, bpr, 48).transpose(0, 2, 1, 3).reshape(-1)
     c = c.reshape(nq, 4, bpr, 8).transpose(0, 2, 1, 3).reshape(-1, 8)
-    return ib, c
+    return sel_layout_np(O.unpack(ib, ib.size * 8 // 3, 3)), c
 
 
 @pytest.mark.parametrize("N,K", [(8, 2048), (2560, 2560), (1001, 6912), (3, 128), (6, 8192)])

@@ -2,8 +2,10 @@
 (nb_gemm_skinny_tile_batched), run with -m gpu.
 
 Bars: the layout is byte-exact against a numpy construction from the
-unpacked indices (tiles of 16 rows x 4 column blocks; in every 32-index
-unit index 4s + t at position o(s) + 8t, o = (0, 1, 3, 4, 6, 7, 2, 5); row
+unpacked indices (tiles of 16 rows x 4 column blocks; every 32-index unit
+the selector-ordered unit (tests/test_stream_layout.py) whose selector s
+holds indices 4s .. 4s + 3, i.e. the unit of the indices placed at
+positions o(s) + 8t, o = (0, 1, 3, 4, 6, 7, 2, 5); row
 r's blocks at block place (b + ((r >> 1) & 3) + (r >> 3)) & 3, its codebook
 pieces p at place (p + ((r & 6) | ((r ^ (r >> 3)) & 1))) & 7; zeros past
 the layer); the products are bit-identical to
@@ -19,6 +21,7 @@ from nativebit_amd import ops
 from oracle import oracle as O
 
 from test_gpu_parity import REL_F32, note, random_layer, ref_gemv, rel
+from test_stream_layout import sel_layout_np
 
 pytestmark = pytest.mark.gpu
 
@@ -35,7 +38,7 @@ def tile_layout_np(idx, cb, N, K):
     so = np.empty_like(u)
     for i in range(32):
         so[:, SEL_OFFSET[i >> 2] + 8 * (i & 3)] = u[:, i]
-    blocks = O.pack(so.reshape(-1), 3).reshape(N, bpr, 48)
+    blocks = sel_layout_np(so.reshape(-1)).reshape(N, bpr, 48)
     ib = np.zeros((ng * 16, ns * 4, 48), np.uint8)
     ib[:N, :bpr] = blocks
     c = np.zeros((ng * 16, ns * 4, 8), np.float32)
