@@ -37,8 +37,10 @@ configurations are reported in the same JSON line under "configs":
            2048 tokens, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA
            peak, beside torch's dense bf16 matmul of an unpacked weight
   skinny   config 2: M = 1, 2, 4, 8, 16 activation rows over all 182 matmuls,
-           one batched launch per step (nb_gemm_skinny_batched at M > 1),
-           beside 182 per-matmul nb_gemv launches
+           one batched launch per step (M = 1 on the selector-ordered unit
+           layout, M = 2..4 on the row-quad layout, M > 4 on the tile
+           layout, each beside the same launch on the original layout),
+           and 182 per-matmul nb_gemv launches
   quantize nb_quantize_pack: nearest-entry quantization straight into the
            3-bit stream for one 6912x2560 layer (GB/s), beside the
            reference's distance-tensor formulation on the GPU
@@ -596,8 +598,9 @@ def bench_prefill(dev, random_weights=False):
 def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
     """Config 2: M activation rows over all 182 matmuls of a step.
 
-    batched: one launch per step -- nb_gemv_batched (the streaming kernel)
-    at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2..4
+    batched: one launch per step -- nb_gemv_batched_sel (the streaming
+    kernel, on the selector-ordered unit layout made once by
+    nb_stream_layout) at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2..4
     (the layers re-ordered once by nb_quad_layout, outside the timing, as
     at model load), nb_gemm_skinny_tile_batched on the tile layout at M > 4
     (nb_tile_layout, likewise once) -- replayed as a HIP graph;
@@ -609,6 +612,7 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
     quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats] \
         if any(2 <= M <= 4 for M in ms) else []
     tiles = [ops.tile_layout(m.packed, m.cb, m.N, m.K) for m in mats] if max(ms) > 4 else []
+    sels = [ops.stream_layout(m.packed, m.N, m.K) for m in mats] if 1 in ms else []
     torch.cuda.synchronize()
     out = {}
     for M in ms:
@@ -623,7 +627,19 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
         ms_rows = graph_time(batch.run, 20, 5)
         ms_b, kernel = ms_rows, "gemv_stream_kernel" if M == 1 else "gemv_skinny_kernel"
         extra = {}
-        if 2 <= M <= 4:
+        if M == 1:
+            ysl = [torch.empty(m.N, device=dev) for m in mats]
+            lbatch = ops.GemvBatch([(xs[m.K][0], p, m.cb, y, m.N, m.K)
+                                    for m, p, y in zip(mats, sels, ysl)], layout="sel")
+            ms_b = graph_time(lbatch.run, 20, 5)
+            kernel = "gemv_stream_kernel (selector-ordered unit layout)"
+            # the same selectors in the same order: the same bits
+            if not all(torch.equal(a, b[0]) for a, b in zip(ysl, ys)):
+                raise RuntimeError("skinny M=1: selector-ordered and original layouts disagree")
+            extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
+                     "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
+            del ysl, lbatch
+        elif 2 <= M <= 4:
             yq = [torch.empty(M, m.N, device=dev) for m in mats]
             qbatch = ops.GemvBatch([(xs[m.K], q[0], q[1], y, m.N, m.K)
                                     for m, q, y in zip(mats, quads, yq)], m=M, layout="quad")
@@ -660,12 +676,14 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
         log(f"[bench] skinny M={M}: batched {ms_b*1e3:.1f} us ({nbytes/ms_b/1e6:.0f} GB/s, "
             f"{kernel}), per-matmul launches {ms_p*1e3:.1f} us")
         del ys, xs, batch
-    out["note"] = ("batched: every matmul of the step in one launch (graph replay); M = 2..4 "
+    out["note"] = ("batched: every matmul of the step in one launch (graph replay); M = 1 on "
+                   "the selector-ordered unit layout (nb_stream_layout, once, untimed; "
+                   "bit-identical to the original layout's products), M = 2..4 "
                    "on the row-quad layout (nb_quad_layout, once, untimed), M > 4 on the "
                    "tile layout (nb_tile_layout, once, untimed; bit-identical to the "
                    "original layout's products), rows_layout the same products on the "
                    "original layout; per_matmul: 182 nb_gemv launches per step in one graph")
-    del quads, tiles
+    del quads, tiles, sels
     return out
 
 
