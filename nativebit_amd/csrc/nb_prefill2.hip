@@ -392,8 +392,10 @@ struct PrefillPlan {
 // partial products (written, then read once by the reduction) of at most
 // twice the packed weight's bytes, else four times.  Measured on MI355X
 // over the four 2.2B layer shapes: M = 128 layer 140 -> 86 us, M = 512
-// 191 -> 156-162 us (down 75 -> 44-45 us), M = 2048 unchanged (no split);
-// splitting tiles that already fill the grid was slower.
+// 191 -> 156-162 us (down 75 -> 44-45 us); splitting tiles that already
+// fill the grid was slower.  A tile that reaches 0.6 per CU but leaves more
+// than a tenth of the CUs idle gives way to 256 x 256 over S K ranges when
+// K is long (below).
 PrefillPlan prefill_plan(int M, int N, int K, bool allow_split) {
     const int64_t cus = device_cu_count();
     const int64_t want = cus * 3 / 5;
@@ -404,7 +406,19 @@ PrefillPlan prefill_plan(int M, int N, int K, bool allow_split) {
     };
     const int tiles[4][2] = {{256, 256}, {256, 128}, {128, 128}, {64, 128}};
     for (int t = 0; t < 3; ++t) {
-        if (groups(tiles[t][0], tiles[t][1]) >= want) return {tiles[t][0], tiles[t][1], 1};
+        const int64_t g = groups(tiles[t][0], tiles[t][1]);
+        if (g < want) continue;
+        // A long K on a grid that still leaves a tenth of the CUs idle: the
+        // 256 x 256 tile over S K ranges of at least 32 steps, where that
+        // gives more workgroups (down at M = 2048: 160 tiles of 256 x 128
+        // 126-135 us, 3 x 80 of 256 x 256 92-98 us; o, whose K ranges would
+        // be 13 steps, stays at 51-54 us unsplit).
+        if (allow_split && M >= 256 && g * 10 < cus * 9) {
+            const int64_t g2 = groups(256, 256);
+            const int S = (int)std::min<int64_t>(cus / g2, nsteps / 32);
+            if (S >= 2 && g2 * S > g) return {256, 256, S};
+        }
+        return {tiles[t][0], tiles[t][1], 1};
     }
     if (allow_split) {
         for (int64_t mult = 2; mult <= 4; mult += 2) {
