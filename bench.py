@@ -62,14 +62,6 @@ import statistics
 import sys
 import time
 
-# Kernel arguments in device memory, a HIP runtime setting read when the
-# runtime starts (so before torch): a graph replay's dispatch then reads its
-# arguments from HBM rather than host memory.  The kernels and their work
-# are unchanged; measured on the single-launch replay, about 1.8 % less time
-# per replay (the launch gap), and no change in the decode schedule.  An
-# explicit setting in the environment wins.
-os.environ.setdefault("HIP_FORCE_DEV_KERNARG", "1")
-
 import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -982,7 +974,6 @@ def main():
                                 "first ~1 ms runs at full clocks, then the power controller "
                                 "throttles for ~20 ms before it settles; the timed region "
                                 "above starts after that"),
-            "hip_runtime": {"HIP_FORCE_DEV_KERNARG": os.environ.get("HIP_FORCE_DEV_KERNARG")},
         },
         "parity": {"spot_check_rel_err_vs_f64": err},
     }

@@ -370,6 +370,11 @@ void gemv_stream_kernel(
     __syncthreads();
 
     // ---- steady state -------------------------------------------------------
+    // A wait the compiler sees: its scoreboard otherwise still counts the
+    // staging loads above as pending (their registers are reused in the
+    // loop), and it would wait for every vector-memory operation -- the
+    // ring's loads too -- at that reuse in every step.
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0), expcnt and lgkmcnt not waited
     if (ma.valid) {
         int ci = -1;  // problem whose fields are in CP
         Prob CP = {};
