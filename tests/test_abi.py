@@ -367,11 +367,14 @@ def prefill_split(**kw):
 
 def test_prefill_split_ws_bytes():
     """K ranges (fp32 partial products M x N each) only where the tile grid
-    would leave CUs idle: few tokens, narrow layers; none at M = 2048."""
+    would leave CUs idle: few tokens, narrow layers; at M = 2048 only the
+    long-K down projection (three ranges of the 256 x 256 tile on a
+    256-CU device: 80 tiles x 3 instead of 160 tiles of 256 x 128)."""
     lib = _lib.load()
     b = lib.nb_gemm_prefill_split_ws_bytes
     for N, K in ((7680, 2560), (2560, 2560), (13824, 2560), (2560, 6912)):
-        assert b(2048, N, K) == 0 and b(1024, N, K) == 0
+        assert b(1024, N, K) == 0
+        assert b(2048, N, K) == (3 * 2048 * N * 4 if K == 6912 else 0)
         s = b(128, N, K)
         assert s > 0 and s % (128 * N * 4) == 0 and 2 <= s // (128 * N * 4) <= 8
         # partial products at most four times the packed weight's bytes
