@@ -110,6 +110,85 @@ struct Prefill2Args {
     int accumulate;  // fp32 y only: y += result instead of y = result
 };
 
+// Tile of the calling workgroup.  Workgroups are dealt to the 8 XCDs in
+// turn (workgroup g to XCD g % 8), each XCD with its own L2: XCD x takes a
+// contiguous run of the tiles in (token tile, output tile) order, so its
+// workgroups share one or two token tiles of X in its L2 rather than all of
+// them.  With a K split, virtual tile v is K range v / ntiles of output
+// tile v % ntiles, so an XCD's run holds neighbouring tiles of one K range
+// (which share their X slices).
+struct TileOf {
+    int n0, m0;       // first output and first token of the tile
+    int ks;           // K range of this workgroup
+    int s0, nsteps;   // its K steps: [s0, s0 + nsteps) of the K / 64
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ TileOf tile_of(const Prefill2Args& a) {
+    const int nn = (a.N + BN - 1) / BN;
+    const int ntiles = nn * ((a.M + BM - 1) / BM);
+    const int T = gridDim.x, g = blockIdx.x, full = T / 8, rem = T % 8, x = g % 8;
+    const int v = x * full + min(x, rem) + g / 8;
+    TileOf t;
+    t.ks = v / ntiles;
+    const int tile = v - t.ks * ntiles;
+    t.n0 = (tile % nn) * BN;
+    t.m0 = (tile / nn) * BM;
+    t.s0 = (int)((int64_t)t.ks * (a.K / kBK) / a.ksplit);
+    t.nsteps = (int)((int64_t)(t.ks + 1) * (a.K / kBK) / a.ksplit) - t.s0;
+    return t;
+}
+
+// Epilogue: D fragment (i, j) of a wave whose A sub-tiles start at output
+// nb and B sub-tiles at token mb -- the lane holds outputs
+// nb + 16 i + 4 fq .. + 3 for token mb + 16 j + fr.  With a K split, the
+// fp32 partial products go to plane ks of `part` (row stride N), summed by
+// prefill_reduce_kernel.
+template <int TI, int TJ>
+__device__ __forceinline__ void store_tile(const Prefill2Args& a, const f32x4_t (&acc)[TI][TJ],
+                                           int nb, int mb, int fq, int fr, int ks) {
+    const bool partial = a.part != nullptr;
+    const int y_dtype = partial ? NB_F32 : a.y_dtype;
+    void* const yb = partial ? static_cast<void*>(a.part + (int64_t)ks * a.M * a.N) : a.y;
+    const int64_t ldy = partial ? a.N : a.ldy;
+#pragma unroll
+    for (int i = 0; i < TI; ++i) {
+        const int n = nb + i * 16 + fq * 4;
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int m = mb + j * 16 + fr;
+            if (m >= a.M) continue;
+            const f32x4_t v = acc[i][j];
+            if (y_dtype == NB_BF16) {
+                bf16_bits* yp = static_cast<bf16_bits*>(yb) + (int64_t)m * ldy + n;
+                // one 8-byte store where the four outputs exist and the
+                // address allows it (y may be any 2-byte-aligned view)
+                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
+                    u32x2_t p;
+                    p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
+                    p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
+                    *reinterpret_cast<u32x2_t*>(yp) = p;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) yp[e] = f32_to_bf16_rne(v[e]);
+                }
+            } else {
+                float* yp = static_cast<float*>(yb) + (int64_t)m * ldy + n;
+                const bool acc_y = !partial && a.accumulate;
+                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
+                    *reinterpret_cast<f32x4_t*>(yp) =
+                        acc_y ? *reinterpret_cast<const f32x4_t*>(yp) + v : v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (n + e < a.N) yp[e] = acc_y ? yp[e] + v[e] : v[e];
+                }
+            }
+        }
+    }
+}
+
 // One thread's share of a W slice: 12 index bytes (32 weights) per half
 // row it takes (H = 1 or 2) and the codebook of the row's block.  Each
 // 12-byte piece is one register tuple, so its loads land in place without
@@ -140,28 +219,9 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
     using WR = WRegs<H>;
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Tile of this workgroup.  Workgroups are dealt to the 8 XCDs in turn
-    // (workgroup g to XCD g % 8), each XCD with its own L2: XCD x takes a
-    // contiguous run of the tiles in (token tile, output tile) order, so
-    // its workgroups share one or two token tiles of X in its L2 rather
-    // than all of them.
-    // With a K split, virtual tile v is K range v / ntiles of output tile
-    // v % ntiles, so an XCD's run holds neighbouring tiles of one K range
-    // (which share their X slices).
-    const int nn = (a.N + BN - 1) / BN;
-    const int ntiles = nn * ((a.M + BM - 1) / BM);
-    int tile, ks;
-    {
-        const int T = gridDim.x, g = blockIdx.x, full = T / 8, rem = T % 8, x = g % 8;
-        const int v = x * full + min(x, rem) + g / 8;
-        ks = v / ntiles;
-        tile = v - ks * ntiles;
-    }
-    const int n0 = (tile % nn) * BN, m0 = (tile / nn) * BM;
+    const TileOf t = tile_of<BM, BN>(a);
+    const int n0 = t.n0, m0 = t.m0, ks = t.ks, s0 = t.s0, nsteps = t.nsteps;
     const int bpr = a.K / 128;
-    // this workgroup's K steps: [s0, s0 + nsteps) of the K / 64
-    const int s0 = (int)((int64_t)ks * (a.K / kBK) / a.ksplit);
-    const int nsteps = (int)((int64_t)(ks + 1) * (a.K / kBK) / a.ksplit) - s0;
     const uint32_t base = lds_addr(smem);
 
     // X slice: instruction i of wave w covers slice rows 8 (kXLoads w + i)
@@ -287,50 +347,7 @@ __global__ __launch_bounds__(64 * WAVES) void prefill2_kernel(Prefill2Args a) {
         if (step + 1 < nsteps) run_step(step + 1, std::integral_constant<int, 1>{}, wq1, wq0);
     }
 
-    // D fragment (i, j): lane holds outputs n = 4 fq .. 4 fq + 3 of A sub-tile
-    // i for token fr of B sub-tile j.  With a K split, the fp32 partial
-    // products go to plane ks of `part` (row stride N), summed by
-    // prefill_reduce_kernel.
-    const bool partial = a.part != nullptr;
-    const int y_dtype = partial ? NB_F32 : a.y_dtype;
-    void* const yb = partial ? static_cast<void*>(a.part + (int64_t)ks * a.M * a.N) : a.y;
-    const int64_t ldy = partial ? a.N : a.ldy;
-#pragma unroll
-    for (int i = 0; i < TI; ++i) {
-        const int n = n0 + wn * WN + i * 16 + fq * 4;
-#pragma unroll
-        for (int j = 0; j < TJ; ++j) {
-            const int m = m0 + wm * WM + j * 16 + fr;
-            if (m >= a.M) continue;
-            const f32x4_t v = acc[i][j];
-            if (y_dtype == NB_BF16) {
-                bf16_bits* yp = static_cast<bf16_bits*>(yb) + (int64_t)m * ldy + n;
-                // one 8-byte store where the four outputs exist and the
-                // address allows it (y may be any 2-byte-aligned view)
-                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 7) == 0) {
-                    u32x2_t p;
-                    p.x = (uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16);
-                    p.y = (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16);
-                    *reinterpret_cast<u32x2_t*>(yp) = p;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < a.N) yp[e] = f32_to_bf16_rne(v[e]);
-                }
-            } else {
-                float* yp = static_cast<float*>(yb) + (int64_t)m * ldy + n;
-                const bool acc_y = !partial && a.accumulate;
-                if (n + 3 < a.N && (reinterpret_cast<uintptr_t>(yp) & 15) == 0) {
-                    *reinterpret_cast<f32x4_t*>(yp) =
-                        acc_y ? *reinterpret_cast<const f32x4_t*>(yp) + v : v;
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        if (n + e < a.N) yp[e] = acc_y ? yp[e] + v[e] : v[e];
-                }
-            }
-        }
-    }
+    store_tile<TI, TJ>(a, acc, n0 + wn * WN, m0 + wm * WM, fq, fr, ks);
 }
 
 // y[m][n] = sum over k ranges s = 0, 1, ... of part[s][m][n] (in that
