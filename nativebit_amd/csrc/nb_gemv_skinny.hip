@@ -7,10 +7,15 @@
 // 258-275) in its bf16 form (inference/eval_ppl.py:149-174) for the few
 // token rows of a small-batch decode step, over all layers of the step.
 //
-// Work split.  A task is 128 rows of one problem over all of K, taken in
-// slices of 512 (4 blocks of 128); wave w of a workgroup owns rows 16w ..
-// 16w + 15 of the task.  The grid is one workgroup per CU, each walking a
-// contiguous range of tasks balanced by slice count, so a workgroup's loads
+// Work split.  A task is 128 R rows of one problem over all of K, taken in
+// slices of 512 (4 blocks of 128); an item is one 128-row half (h = 0 .. R
+// - 1) of one slice, items in (slice, h) order, and wave w of a workgroup
+// owns rows 128 h + 16w .. + 15 of the task in item (s, h).  The R items of
+// a slice share one x slice, so the workgroup loads x once per R x 40 KiB
+// of weights (with the MFMAs removed, the kernel's time follows the bytes
+// it brings into LDS, x included: 221 / 274 us at M = 5 / 16 for 45 / 56
+// KiB per item).  The grid is one workgroup per CU, each walking a
+// contiguous range of tasks balanced by item count, so a workgroup's loads
 // run on from one task into the next without a ramp.
 //
 // Memory side.  Each wave keeps a ring of three LDS slots, one slice each
@@ -56,6 +61,7 @@
 // Weights are rounded to bf16 (RNE), as the reference's bf16 path;
 // accumulation is fp32.
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 #include "nb_device.h"
@@ -76,9 +82,15 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 #ifndef NB_SK_DEPTH
 #define NB_SK_DEPTH 3
 #endif
+#ifndef NB_SK_R
+#define NB_SK_R 2
+#endif
 constexpr int kSkWaves = NB_SK_WAVES;
 constexpr int kSkThreads = 64 * kSkWaves;
-constexpr int kSkRows = 16 * kSkWaves;         // rows of one task
+constexpr int kSkRows = 16 * kSkWaves;         // rows of one item
+constexpr int kSkR = NB_SK_R;                  // items per slice of a task
+constexpr int kSkTaskRows = kSkRows * kSkR;    // rows of one task
+static_assert(kSkR >= 1 && kSkR <= 4, "one to four 128-row items per slice");
 constexpr int kSkSliceK = 512;                 // K of one slice (4 blocks)
 constexpr int kSkMaxM = 16;
 constexpr int kSkXRow = kSkSliceK * 2;         // LDS bytes of one staged x row
@@ -271,6 +283,7 @@ struct Cursor {
     int p;        // problem index (relative to tasks.prob0)
     int task;     // task index of the launch
     int s;        // slice of the task
+    int h;        // 128-row half of the task (item (s, h))
     int ns;       // slices of the problem
     int row0;     // first row of the wave's group
     int N, K, bpr;
@@ -299,10 +312,11 @@ __device__ __forceinline__ void cursor_load(const SkinnyArgs& a, Cursor& c) {
 }
 
 __device__ __forceinline__ void cursor_rows(const SkinnyArgs& a, Cursor& c, int wave) {
-    c.row0 = (c.task - a.tasks.task_begin[c.p]) * kSkRows + wave * 16;
+    c.row0 = (c.task - a.tasks.task_begin[c.p]) * kSkTaskRows + c.h * kSkRows + wave * 16;
 }
 
-__device__ __forceinline__ void cursor_next(const SkinnyArgs& a, Cursor& c, int wave) {
+// the next slice (h stays 0: the x cursor, one step per slice)
+__device__ __forceinline__ void cursor_next_slice(const SkinnyArgs& a, Cursor& c, int wave) {
     if (++c.s < c.ns) return;
     c.s = 0;
     ++c.task;
@@ -311,6 +325,17 @@ __device__ __forceinline__ void cursor_next(const SkinnyArgs& a, Cursor& c, int 
         cursor_load(a, c);
     }
     cursor_rows(a, c, wave);
+}
+
+// the next item
+__device__ __forceinline__ void cursor_next(const SkinnyArgs& a, Cursor& c, int wave) {
+    if (++c.h < kSkR) {
+        cursor_rows(a, c, wave);
+        return;
+    }
+    c.h = 0;
+    cursor_rows(a, c, wave);
+    cursor_next_slice(a, c, wave);
 }
 
 template <int NXB, bool TILE>
@@ -336,6 +361,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         cc.p = lo;
         cc.task = t0;
         cc.s = 0;
+        cc.h = 0;
         cursor_load(a, cc);
         cursor_rows(a, cc, wave);
     }
@@ -348,7 +374,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
                 ++c.p;
                 cursor_load(a, c);
             }
-            nitems += c.ns;
+            nitems += c.ns * kSkR;
         }
     }
 
@@ -382,11 +408,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         w_blk[3 + i] = piece >> 1;
         w_off[3 + i] = (piece & 1) * 16;
     }
-    // Row bases of the weight loads of the W cursor's task (recomputed when
-    // the task changes): per load, the row's first index byte or codebook
+    // Row bases of the weight loads of the W cursor's item rows (recomputed
+    // when they change): per load, the row's first index byte or codebook
     // byte plus the lane's offset inside a block.
     const unsigned char* wbase[5];
-    int wtask = -1;
+    int wtask = -1, wh = -1;
     auto w_rows = [&](const Cursor& c) {
 #pragma unroll
         for (int i = 0; i < 5; ++i) {
@@ -396,6 +422,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
                                    w_off[i];
         }
         wtask = c.task;
+        wh = c.h;
     };
     auto issue_w = [&](const Cursor& c, int slot) {
         const uint32_t dst = __builtin_amdgcn_readfirstlane(ring + slot * kSkSlot);
@@ -414,7 +441,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             dma16_nt(dst + 3072, cp);
             dma16_nt(dst + 4096, cp + 1024);
         } else {
-            if (c.task != wtask) w_rows(c);
+            if (c.task != wtask || c.h != wh) w_rows(c);
 #pragma unroll
             for (int i = 0; i < 5; ++i) {
                 const int blk = min(4 * c.s + w_blk[i], c.bpr - 1);
@@ -422,7 +449,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             }
         }
     };
-    // x slice of item c into buffer `buf`: wave w loads activation rows
+    // x slice of slice c.s into buffer `buf`: wave w loads activation rows
     // min(2w + j, M - 1), j = 0, 1 -- always two loads, so the wait counts
     // below are exact (a clamped row rewrites row M - 1 with the same bytes,
     // before anyone reads that buffer).  Lane l takes the 16 bytes of
@@ -449,11 +476,14 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     const int cb_off1 = kSkIdxBytes + r * 128 + ((2 * q + 1 + cb_rot(r)) & 7) * 16;
     const int x_off = xm * kSkXRow;
     const int x_swz = xm & 15;
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    // one accumulator per 128-row half of the task
+    f32x4_t acc[kSkR];
+#pragma unroll
+    for (int h = 0; h < kSkR; ++h) acc[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     // A finished task's outputs wait in `pend` and are stored after the
-    // next item's loads are issued.  acc lane (q, r) holds C[4q + v][r]:
-    // y[r][row0 + 4q + v].
-    f32x4_t pend = acc;
+    // next item's loads are issued.  acc[h] lane (q, r) holds C[4q + v][r]:
+    // y[r][row0 + 128 h + 4q + v], row0 the first row of the wave in half 0.
+    f32x4_t pend[kSkR];
     int pend_p = 0, pend_row0 = 0, pend_n = 0;
     bool pending = false;
     auto store = [&]() {
@@ -463,61 +493,83 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         const bool add = P->y_mode == NB_Y_ADD;
         void* y = P->y;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = pend_row0 + 4 * q + v;
-            if (n >= pend_n) continue;
-            const int64_t yi = (int64_t)r * pend_n + n;
-            if (a.y_dtype == NB_BF16) {
-                *as_global_mut(static_cast<bf16_bits*>(y) + yi) = f32_to_bf16_rne(pend[v]);
-            } else if (add) {
-                auto* yp = as_global_mut(static_cast<float*>(y) + yi);
-                *yp = *yp + pend[v];
-            } else {
-                *as_global_mut(static_cast<float*>(y) + yi) = pend[v];
+        for (int h = 0; h < kSkR; ++h) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int n = pend_row0 + h * kSkRows + 4 * q + v;
+                if (n >= pend_n) continue;
+                const int64_t yi = (int64_t)r * pend_n + n;
+                if (a.y_dtype == NB_BF16) {
+                    *as_global_mut(static_cast<bf16_bits*>(y) + yi) =
+                        f32_to_bf16_rne(pend[h][v]);
+                } else if (add) {
+                    auto* yp = as_global_mut(static_cast<float*>(y) + yi);
+                    *yp = *yp + pend[h][v];
+                } else {
+                    *as_global_mut(static_cast<float*>(y) + yi) = pend[h][v];
+                }
             }
         }
     };
 
     // ---- the pipeline -----------------------------------------------------
-    // Item i's loads are X(i) (the x slice, two loads, into buffer
-    // i % NXB) and W(i) (the wave's weight slice, five loads, into slot
-    // i % kSkDepth).  Step j (j = -kSkDepth .. -1 before the loop, then
-    // item j's step) issues X(j + kLead), then W(j + kSkDepth), where they
-    // exist.  Item i's step waits until W(i) and X(i) are in, passes the
-    // workgroup barrier (every wave's x pieces of item i are in, and every
-    // wave is done with item i - 1, whose x buffer X(i + kLead) refills),
-    // reads slot i into registers, issues X(i + kLead), computes, and then
-    // issues W(i + kSkDepth) into the slot it read.  kSkDepth slices of weights
+    // Item i's weights W(i) (five loads) go to slot i % kSkDepth; slice g's x
+    // X(g) (two loads, g = i / R for item i) to buffer g % NXB.  Before the
+    // loop: X(0 .. kLead - 1), then W(0 .. kSkDepth - 1).  Item i's step
+    // waits until W(i) is in -- and for the first item of a slice X(g) too,
+    // then passes the workgroup barrier (every wave's x pieces of slice g
+    // are in, and every wave is done with slice g - 1, whose x buffer
+    // X(g + kLead) refills) -- reads slot i into registers, issues
+    // X(g + kLead) (first item of a slice), computes, and then issues
+    // W(i + kSkDepth) into the slot it read.  kSkDepth slices of weights
     // are in flight while one is computed.  Loads complete in issue order,
-    // so W(i) and X(i) are in once at most after(i) loads are outstanding:
-    // those issued after X(i) (the later of the two; kLead <= kSkDepth).
-    // (Output stores, issued after an item's loads, only make the waits
-    // longer.)
-    constexpr int kLead = NXB - 1;  // steps between X's issue and use
-    static_assert(kLead <= kSkDepth, "x is requested no earlier than the weights");
+    // so what a step needs is in once at most after(i) loads are
+    // outstanding: those issued after the later of W(i) and X(g).  (Output
+    // stores, issued after a step's loads, only make the waits longer.)
+    constexpr int kLead = NXB - 1;  // slices between X's issue and use
+    const int nslices = nitems / kSkR;
+    auto x_at = [&](int j) {  // x loads issued in step j
+        return (j % kSkR == 0 && j / kSkR + kLead < nslices) ? 2 : 0;
+    };
+    auto w_at = [&](int j) { return j + kSkDepth < nitems ? 5 : 0; };  // in step j
     auto after = [&](int i) {
-        const int j0 = i - kLead;  // the step that issued X(i)
-        int n = (kLead < kSkDepth && j0 + kSkDepth < nitems) ? 5 : 0;
-        for (int j = j0 + 1; j < i; ++j) {
-            n += (j + kLead < nitems ? 2 : 0) + (j + kSkDepth < nitems ? 5 : 0);
+        int nw = 0;  // loads issued after W(i)
+        if (i < kSkDepth) {
+            for (int d = i + 1; d < kSkDepth && d < nitems; ++d) nw += 5;
+            for (int j = 0; j < i; ++j) nw += x_at(j) + w_at(j);
+        } else {
+            for (int j = i - kSkDepth + 1; j < i; ++j) nw += x_at(j) + w_at(j);
         }
-        return n;
+        if (i % kSkR != 0) return nw;
+        const int g = i / kSkR;
+        int nx = 0;  // loads issued after X(g)
+        if (g < kLead) {
+            for (int gg = g + 1; gg < kLead && gg < nslices; ++gg) nx += 2;
+            for (int d = 0; d < kSkDepth && d < nitems; ++d) nx += 5;
+            for (int j = 0; j < i; ++j) nx += x_at(j) + w_at(j);
+        } else {
+            const int j0 = (g - kLead) * kSkR;  // the step that issued X(g)
+            nx = w_at(j0);
+            for (int j = j0 + 1; j < i; ++j) nx += x_at(j) + w_at(j);
+        }
+        return min(nw, nx);
     };
     Cursor cx = cc, cw = cc;
-    for (int j = -kSkDepth; j < 0; ++j) {
-        if (j + kLead >= 0 && j + kLead < nitems) {
-            issue_x(cx, (j + kLead) % NXB);
-            cursor_next(a, cx, wave);
-        }
-        if (j + kSkDepth < nitems) {
-            issue_w(cw, j + kSkDepth);
-            cursor_next(a, cw, wave);
-        }
+    for (int g = 0; g < kLead && g < nslices; ++g) {
+        issue_x(cx, g % NXB);
+        cursor_next_slice(a, cx, wave);
+    }
+    for (int d = 0; d < kSkDepth && d < nitems; ++d) {
+        issue_w(cw, d);
+        cursor_next(a, cw, wave);
     }
 
-    for (int i = 0; i < nitems; ++i) {
+    // item i (half H of its slice) into acc[H]
+    auto step = [&](int i, auto h_c) {
+        constexpr int H = decltype(h_c)::value;
+        const int g = i / kSkR;
         wait_vm_n(after(i));
-        wg_barrier();
+        if (H == 0) wg_barrier();
         // ---- slot i into registers, then this step's loads ----
         const int si = i % kSkDepth;
         const unsigned char* slot = ring_p + si * kSkSlot;
@@ -537,12 +589,12 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         const f32x4_t c1 = *reinterpret_cast<const f32x4_t*>(slot + cb_off1);
         // the slot's bytes are in registers before its refill is issued
         asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
-        if (i + kLead < nitems) {
-            issue_x(cx, (i + kLead) % NXB);
-            cursor_next(a, cx, wave);
+        if (H == 0 && g + kLead < nslices) {
+            issue_x(cx, (g + kLead) % NXB);
+            cursor_next_slice(a, cx, wave);
         }
         if (pending) store();
-        // ---- compute slice cc.s of the task ----
+        // ---- compute item (cc.s, H) of the task ----
         const bool live = cc.row0 + r < cc.N && 4 * cc.s + q < cc.bpr;
         const uint32_t p0 = pack_bf16x2(c0.x, c0.y);
         const uint32_t p1 = pack_bf16x2(c0.z, c0.w);
@@ -556,11 +608,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         hi0 = live ? hi0 : 0u;
         lo1 = live ? lo1 : 0u;
         hi1 = live ? hi1 : 0u;
-        const unsigned char* xb = smem + kSkRing + (i % NXB) * xbuf_bytes + x_off;
+        const unsigned char* xb = smem + kSkRing + (g % NXB) * xbuf_bytes + x_off;
         if constexpr (TILE) {
-            mfma_units_tile<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+            mfma_units_tile<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc[H]);
         } else {
-            mfma_groups<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc);
+            mfma_groups<0>(d, lo0, lo1, hi0, hi1, xb, q * 16, x_swz, acc[H]);
         }
         // the weights of step i + kSkDepth into the slot read above, after
         // the MFMAs: issued before them, the five loads can stall at issue
@@ -569,15 +621,24 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             issue_w(cw, si);
             cursor_next(a, cw, wave);
         }
-        if (cc.s == cc.ns - 1) {
-            pend = acc;
+        if (H == kSkR - 1 && cc.s == cc.ns - 1) {
+#pragma unroll
+            for (int h = 0; h < kSkR; ++h) {
+                pend[h] = acc[h];
+                acc[h] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
             pend_p = cc.p;
-            pend_row0 = cc.row0;
+            pend_row0 = cc.row0 - H * kSkRows;
             pend_n = cc.N;
             pending = true;
-            acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
         }
         cursor_next(a, cc, wave);
+    };
+    for (int i = 0; i < nitems; i += kSkR) {
+        step(i, std::integral_constant<int, 0>{});
+        if constexpr (kSkR > 1) step(i + 1, std::integral_constant<int, 1>{});
+        if constexpr (kSkR > 2) step(i + 2, std::integral_constant<int, 2>{});
+        if constexpr (kSkR > 3) step(i + 3, std::integral_constant<int, 3>{});
     }
     if (pending) store();
 }
@@ -708,8 +769,8 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
         for (int i = 0; i < n; ++i) {
             A.tasks.task_begin[i] = (int32_t)slices.size();
             const StreamProblem& P = host_probs[p0 + i];
-            const int nt = (P.N + kSkRows - 1) / kSkRows;
-            const int ns = ((P.K >> 7) + 3) >> 2;
+            const int nt = (P.N + kSkTaskRows - 1) / kSkTaskRows;
+            const int ns = (((P.K >> 7) + 3) >> 2) * kSkR;  // items of a task
             for (int t = 0; t < nt; ++t) slices.push_back(ns);
             total_slices += (int64_t)nt * ns;
             max_slices = std::max(max_slices, ns);
