@@ -38,7 +38,7 @@ configurations are reported in the same JSON line under "configs":
            peak, beside torch's dense bf16 matmul of an unpacked weight
   skinny   config 2: M = 1, 2, 4, 8, 16 activation rows over all 182 matmuls,
            one batched launch per step (M = 1 on the selector-ordered unit
-           layout, M = 2..4 on the row-quad layout, M > 4 on the tile
+           layout, M = 2 on the row-quad layout, M > 2 on the tile
            layout, each beside the same launch on the original layout),
            and 182 per-matmul nb_gemv launches
   quantize nb_quantize_pack: nearest-entry quantization straight into the
@@ -600,18 +600,19 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
 
     batched: one launch per step -- nb_gemv_batched_sel (the streaming
     kernel, on the selector-ordered unit layout made once by
-    nb_stream_layout) at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2..4
+    nb_stream_layout) at M = 1, nb_gemm_skinny_quad_batched on the row-quad layout at M = 2
     (the layers re-ordered once by nb_quad_layout, outside the timing, as
-    at model load), nb_gemm_skinny_tile_batched on the tile layout at M > 4
-    (nb_tile_layout, likewise once) -- replayed as a HIP graph;
+    at model load), nb_gemm_skinny_tile_batched on the tile layout at M > 2
+    (nb_tile_layout, likewise once; at M = 3 / 4 it measured 3-4 % faster
+    than the row-quad kernel, at M = 2 about 1 % slower) -- replayed as a
+    HIP graph;
     rows_layout: nb_gemm_skinny_batched on the original layout, for
     comparison; per_matmul: 182 nb_gemv launches per step (one per matmul)
     in a graph."""
     from nativebit_amd import ops, synth
     mats = [mats[name] for mats in layers for name, _, _ in synth.LAYER_SHAPES]
-    quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats] \
-        if any(2 <= M <= 4 for M in ms) else []
-    tiles = [ops.tile_layout(m.packed, m.cb, m.N, m.K) for m in mats] if max(ms) > 4 else []
+    quads = [ops.quad_layout(m.packed, m.cb, m.N, m.K) for m in mats] if 2 in ms else []
+    tiles = [ops.tile_layout(m.packed, m.cb, m.N, m.K) for m in mats] if max(ms) > 2 else []
     sels = [ops.stream_layout(m.packed, m.N, m.K) for m in mats] if 1 in ms else []
     torch.cuda.synchronize()
     out = {}
@@ -639,7 +640,7 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
             extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
                      "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
             del ysl, lbatch
-        elif 2 <= M <= 4:
+        elif M == 2:
             yq = [torch.empty(M, m.N, device=dev) for m in mats]
             qbatch = ops.GemvBatch([(xs[m.K], q[0], q[1], y, m.N, m.K)
                                     for m, q, y in zip(mats, quads, yq)], m=M, layout="quad")
@@ -651,7 +652,7 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
             extra = {"rows_layout_us_per_step": round(ms_rows * 1e3, 1),
                      "rows_layout_GB_s": round(nbytes / ms_rows / 1e6, 1)}
             del yq, qbatch
-        elif M > 4:
+        elif M > 2:
             yq = [torch.empty(M, m.N, device=dev) for m in mats]
             sbatch = ops.GemvBatch([(xs[m.K], t[0], t[1], y, m.N, m.K)
                                     for m, t, y in zip(mats, tiles, yq)], m=M, layout="tile")
@@ -678,8 +679,8 @@ def bench_skinny(dev, layers, ms=(1, 2, 4, 8, 16), per_matmul=True):
         del ys, xs, batch
     out["note"] = ("batched: every matmul of the step in one launch (graph replay); M = 1 on "
                    "the selector-ordered unit layout (nb_stream_layout, once, untimed; "
-                   "bit-identical to the original layout's products), M = 2..4 "
-                   "on the row-quad layout (nb_quad_layout, once, untimed), M > 4 on the "
+                   "bit-identical to the original layout's products), M = 2 "
+                   "on the row-quad layout (nb_quad_layout, once, untimed), M > 2 on the "
                    "tile layout (nb_tile_layout, once, untimed; bit-identical to the "
                    "original layout's products), rows_layout the same products on the "
                    "original layout; per_matmul: 182 nb_gemv launches per step in one graph")
