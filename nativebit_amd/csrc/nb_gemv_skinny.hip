@@ -7,14 +7,15 @@
 // 258-275) in its bf16 form (inference/eval_ppl.py:149-174) for the few
 // token rows of a small-batch decode step, over all layers of the step.
 //
-// Work split.  A task is 128 R rows of one problem over all of K, taken in
-// slices of 512 (4 blocks of 128); an item is one 128-row half (h = 0 .. R
-// - 1) of one slice, items in (slice, h) order, and wave w of a workgroup
-// owns rows 128 h + 16w .. + 15 of the task in item (s, h).  The R items of
-// a slice share one x slice, so the workgroup loads x once per R x 40 KiB
-// of weights (with the MFMAs removed, the kernel's time follows the bytes
-// it brings into LDS, x included: 221 / 274 us at M = 5 / 16 for 45 / 56
-// KiB per item).  The grid is one workgroup per CU, each walking a
+// Work split.  A task is 128 R rows of one problem over all of K (R = 2 on
+// the tile layout, 1 on the reference layout: skinny_r), taken in slices
+// of 512 (4 blocks of 128); an item is one 128-row part (h = 0 .. R - 1) of
+// one slice, items in (slice, h) order, and wave w of a workgroup owns rows
+// 128 h + 16w .. + 15 of the task in item (s, h).  The R items of a slice
+// share one x slice, so the workgroup loads x once per R x 40 KiB of
+// weights (with the MFMAs removed, the kernel's time follows the bytes it
+// brings into LDS, x included: 221 / 274 us at M = 5 / 16 for 45 / 56 KiB
+// per item).  The grid is one workgroup per CU, each walking a
 // contiguous range of tasks balanced by item count, so a workgroup's loads
 // run on from one task into the next without a ramp.
 //
@@ -82,15 +83,13 @@ typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
 #ifndef NB_SK_DEPTH
 #define NB_SK_DEPTH 3
 #endif
-#ifndef NB_SK_R
-#define NB_SK_R 2
-#endif
 constexpr int kSkWaves = NB_SK_WAVES;
 constexpr int kSkThreads = 64 * kSkWaves;
 constexpr int kSkRows = 16 * kSkWaves;         // rows of one item
-constexpr int kSkR = NB_SK_R;                  // items per slice of a task
-constexpr int kSkTaskRows = kSkRows * kSkR;    // rows of one task
-static_assert(kSkR >= 1 && kSkR <= 4, "one to four 128-row items per slice");
+// 128-row items per slice of a task: two on the tile layout; one on the
+// reference layout, whose row bases are re-derived whenever the item's rows
+// change (with two it measured slower: 312 -> 335 us at M = 16)
+__host__ __device__ constexpr int skinny_r(bool tile) { return tile ? 2 : 1; }
 constexpr int kSkSliceK = 512;                 // K of one slice (4 blocks)
 constexpr int kSkMaxM = 16;
 constexpr int kSkXRow = kSkSliceK * 2;         // LDS bytes of one staged x row
@@ -311,11 +310,13 @@ __device__ __forceinline__ void cursor_load(const SkinnyArgs& a, Cursor& c) {
     c.x = static_cast<const uint16_t*>(P->x);
 }
 
+template <int R>
 __device__ __forceinline__ void cursor_rows(const SkinnyArgs& a, Cursor& c, int wave) {
-    c.row0 = (c.task - a.tasks.task_begin[c.p]) * kSkTaskRows + c.h * kSkRows + wave * 16;
+    c.row0 = (c.task - a.tasks.task_begin[c.p]) * (R * kSkRows) + c.h * kSkRows + wave * 16;
 }
 
 // the next slice (h stays 0: the x cursor, one step per slice)
+template <int R>
 __device__ __forceinline__ void cursor_next_slice(const SkinnyArgs& a, Cursor& c, int wave) {
     if (++c.s < c.ns) return;
     c.s = 0;
@@ -324,22 +325,24 @@ __device__ __forceinline__ void cursor_next_slice(const SkinnyArgs& a, Cursor& c
         ++c.p;
         cursor_load(a, c);
     }
-    cursor_rows(a, c, wave);
+    cursor_rows<R>(a, c, wave);
 }
 
 // the next item
+template <int R>
 __device__ __forceinline__ void cursor_next(const SkinnyArgs& a, Cursor& c, int wave) {
-    if (++c.h < kSkR) {
-        cursor_rows(a, c, wave);
+    if (++c.h < R) {
+        cursor_rows<R>(a, c, wave);
         return;
     }
     c.h = 0;
-    cursor_rows(a, c, wave);
-    cursor_next_slice(a, c, wave);
+    cursor_rows<R>(a, c, wave);
+    cursor_next_slice<R>(a, c, wave);
 }
 
 template <int NXB, bool TILE>
 __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
+    constexpr int kSkR = skinny_r(TILE);
     extern __shared__ __align__(16) unsigned char smem[];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -363,7 +366,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         cc.s = 0;
         cc.h = 0;
         cursor_load(a, cc);
-        cursor_rows(a, cc, wave);
+        cursor_rows<kSkR>(a, cc, wave);
     }
     // items (task, slice) of the workgroup
     int nitems = 0;
@@ -557,11 +560,11 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
     Cursor cx = cc, cw = cc;
     for (int g = 0; g < kLead && g < nslices; ++g) {
         issue_x(cx, g % NXB);
-        cursor_next_slice(a, cx, wave);
+        cursor_next_slice<kSkR>(a, cx, wave);
     }
     for (int d = 0; d < kSkDepth && d < nitems; ++d) {
         issue_w(cw, d);
-        cursor_next(a, cw, wave);
+        cursor_next<kSkR>(a, cw, wave);
     }
 
     // item i (half H of its slice) into acc[H]
@@ -591,7 +594,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
         if (H == 0 && g + kLead < nslices) {
             issue_x(cx, (g + kLead) % NXB);
-            cursor_next_slice(a, cx, wave);
+            cursor_next_slice<kSkR>(a, cx, wave);
         }
         if (pending) store();
         // ---- compute item (cc.s, H) of the task ----
@@ -619,7 +622,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
         // behind a full memory queue, and the wave with them
         if (i + kSkDepth < nitems) {
             issue_w(cw, si);
-            cursor_next(a, cw, wave);
+            cursor_next<kSkR>(a, cw, wave);
         }
         if (H == kSkR - 1 && cc.s == cc.ns - 1) {
 #pragma unroll
@@ -632,7 +635,7 @@ __global__ __launch_bounds__(kSkThreads) void gemv_skinny_kernel(SkinnyArgs a) {
             pend_n = cc.N;
             pending = true;
         }
-        cursor_next(a, cc, wave);
+        cursor_next<kSkR>(a, cc, wave);
     };
     for (int i = 0; i < nitems; i += kSkR) {
         step(i, std::integral_constant<int, 0>{});
@@ -769,8 +772,9 @@ int launch_gemv_skinny(const StreamProblem* dev_probs, const StreamProblem* host
         for (int i = 0; i < n; ++i) {
             A.tasks.task_begin[i] = (int32_t)slices.size();
             const StreamProblem& P = host_probs[p0 + i];
-            const int nt = (P.N + kSkTaskRows - 1) / kSkTaskRows;
-            const int ns = (((P.K >> 7) + 3) >> 2) * kSkR;  // items of a task
+            const int R = skinny_r(tile);
+            const int nt = (P.N + R * kSkRows - 1) / (R * kSkRows);
+            const int ns = (((P.K >> 7) + 3) >> 2) * R;  // items of a task
             for (int t = 0; t < nt; ++t) slices.push_back(ns);
             total_slices += (int64_t)nt * ns;
             max_slices = std::max(max_slices, ns);
