@@ -169,3 +169,42 @@ def test_tile_layout_rejects(dev):
     # a reference-layout layer is not a tile-layout one
     with pytest.raises(ValueError):
         ops.GemvBatch([(x, pt, cb, torch.empty(2, 4, device=dev), 4, 128)], m=2, layout="tile")
+
+
+@pytest.mark.parametrize("M", [3, 14])
+def test_tile_skinny_task_runs_cross_items(dev, M):
+    """Many small items on the tile layout: 256-row tasks whose second
+    128-row half is partly or wholly past N (every item with N <= 256),
+    workgroup runs that cross many item boundaries, partial last slices,
+    y += items; every item gives the reference-layout kernel's bits and a
+    spread sample is within the fp64 bar."""
+    n = 160
+    rows, tiles, refs = [], [], []
+    for i in range(n):
+        N, K = 1 + (i * 53) % 300, 128 * (1 + i % 7)
+        idx, p, cb = random_layer(N, K, 3, 8, 128, 8100 + i)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(700 + i))
+        x = x.to(torch.bfloat16).to(dev)
+        pt, ct = torch.from_numpy(p).to(dev), torch.from_numpy(cb).to(dev)
+        tp, tc = ops.tile_layout(pt, ct, N, K)
+        add = i % 4 == 0
+        y0 = torch.randn(M, N, generator=torch.Generator().manual_seed(3 + i)).to(dev)
+        form = ({"y": "add"},) if add else ()
+        rows.append((x, pt, ct, y0.clone() if add else torch.full((M, N), float("nan"),
+                                                                 device=dev), N, K) + form)
+        tiles.append((x, tp, tc, y0.clone() if add else torch.full((M, N), float("nan"),
+                                                                  device=dev), N, K) + form)
+        refs.append((idx, cb, x.cpu(), y0.cpu() if add else None))
+    note(f"tile skinny M={M} with {n} small items")
+    ops.GemvBatch(rows, m=M).run()
+    ops.GemvBatch(tiles, m=M, layout="tile").run()
+    torch.cuda.synchronize()
+    for i in range(n):
+        assert torch.equal(tiles[i][3], rows[i][3]), (i, tiles[i][4], tiles[i][5])
+    for i in range(0, n, 5):
+        idx, cb, x, y0 = refs[i]
+        N, K = tiles[i][4], tiles[i][5]
+        got = tiles[i][3].cpu()
+        if y0 is not None:
+            got = got - y0
+        assert rel(got, ref_gemv(x, idx, cb, 128, N, K)) <= REL_F32, (i, N, K)
