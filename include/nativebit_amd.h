@@ -466,6 +466,22 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
                       int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                       int V, int C, void* stream);
 
+/*
+ * The final RMSNorm and nb_lm_head_argmax in one launch: h = bf16((x /
+ * sqrt(mean(x^2) + eps)) * norm_w) of the fp32 residual x [C] (norm_w fp32
+ * [C]), then the tied head, soft cap and greedy choice exactly as
+ * nb_lm_head_argmax on that h.  Every workgroup forms h itself with
+ * nb_add_rmsnorm's arithmetic, so the logits are bit for bit those of
+ * nb_add_rmsnorm (x unchanged, y and emb NULL) followed by
+ * nb_lm_head_argmax.  Same state, tokens and forcing contract.
+ * Replaces: the final norm, head and argmax of PackedGPT.forward / benchmark
+ *           (inference/generate_torch.py:29-38, 157-159, 311).
+ */
+int nb_rmsnorm_lm_head_argmax(const float* x, const float* norm_w, float eps, const void* emb,
+                              float* logits, nb_decode_state* state, int32_t* tokens_out,
+                              int tokens_cap, const int32_t* force, int n_force, int V, int C,
+                              void* stream);
+
 /* ------------------------------------------------------------------------
  * Batched forward pass over T tokens (a prompt fed as one sequence, as
  * PackedGPT.forward does with T > 1, inference/generate_torch.py:299-302):

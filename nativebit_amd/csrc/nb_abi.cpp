@@ -586,6 +586,29 @@ int nb_tile_layout(const uint8_t* packed, const float* codebook, int N, int K, u
 
 }  // extern "C"
 
+namespace {
+// Shared checks of the head entry points (h: the bf16 input, or the fp32
+// residual when the norm is fused in).
+int check_head(const char* fn, const void* h, const void* emb, float* logits,
+               nb_decode_state* state, int32_t* tokens_out, int tokens_cap,
+               const int32_t* force, int n_force, int V, int C, int h_align) {
+    if (V < 1 || C < 8 || C % 8 || C > lm_head_max_c()) {
+        return fail(NB_EUNSUPPORTED, "%s: V=%d C=%d (C %% 8 == 0, 8 <= C <= %d)", fn, V, C,
+                    lm_head_max_c());
+    }
+    if (!h || !emb || !state) return fail(NB_EINVAL, "%s: NULL pointer", fn);
+    if (n_force < 0 || (n_force > 0 && !force)) return fail(NB_EINVAL, "%s: n_force=%d without force", fn, n_force);
+    if (tokens_cap < 0 || (tokens_cap > 0 && !tokens_out)) {
+        return fail(NB_EINVAL, "%s: tokens_cap=%d without tokens_out", fn, tokens_cap);
+    }
+    if (!aligned(h, h_align) || !aligned(emb, 16) || (logits && !aligned(logits, 4)) ||
+        !aligned(state, 8) || (tokens_out && !aligned(tokens_out, 4))) {
+        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
+    }
+    return NB_OK;
+}
+}  // namespace
+
 extern "C" {
 
 int nb_add_rmsnorm(float* x, const float* y, const float* emb, const nb_decode_state* state,
@@ -776,27 +799,32 @@ int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream) 
     return launch_silu_mul(gu, act, act_dtype, n, static_cast<hipStream_t>(stream));
 }
 
+int nb_rmsnorm_lm_head_argmax(const float* x, const float* norm_w, float eps, const void* emb,
+                              float* logits, nb_decode_state* state, int32_t* tokens_out,
+                              int tokens_cap, const int32_t* force, int n_force, int V, int C,
+                              void* stream) {
+    const char* fn = "nb_rmsnorm_lm_head_argmax";
+    int st = check_head(fn, x, emb, logits, state, tokens_out, tokens_cap, force, n_force, V, C, 4);
+    if (st) return st;
+    if (!norm_w) return fail(NB_EINVAL, "%s: norm_w is NULL", fn);
+    if (!aligned(norm_w, 4)) return fail(NB_EALIGN, "%s: norm_w not 4-byte aligned", fn);
+    if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(NB_EINVAL, "%s: eps=%g", fn, (double)eps);
+    st = ensure_device();
+    if (st) return st;
+    return launch_lm_head_argmax(nullptr, x, norm_w, eps, emb, logits, state, tokens_out,
+                                 tokens_cap, force, n_force, V, C, static_cast<hipStream_t>(stream));
+}
+
 int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* state,
                       int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                       int V, int C, void* stream) {
     const char* fn = "nb_lm_head_argmax";
-    if (V < 1 || C < 8 || C % 8 || C > lm_head_max_c()) {
-        return fail(NB_EUNSUPPORTED, "%s: V=%d C=%d (C %% 8 == 0, 8 <= C <= %d)", fn, V, C,
-                    lm_head_max_c());
-    }
-    if (!h || !emb || !state) return fail(NB_EINVAL, "%s: NULL pointer", fn);
-    if (n_force < 0 || (n_force > 0 && !force)) return fail(NB_EINVAL, "%s: n_force=%d without force", fn, n_force);
-    if (tokens_cap < 0 || (tokens_cap > 0 && !tokens_out)) {
-        return fail(NB_EINVAL, "%s: tokens_cap=%d without tokens_out", fn, tokens_cap);
-    }
-    if (!aligned(h, 2) || !aligned(emb, 16) || (logits && !aligned(logits, 4)) ||
-        !aligned(state, 8) || (tokens_out && !aligned(tokens_out, 4))) {
-        return fail(NB_EALIGN, "%s: misaligned pointer", fn);
-    }
-    int st = ensure_device();
+    int st = check_head(fn, h, emb, logits, state, tokens_out, tokens_cap, force, n_force, V, C, 2);
     if (st) return st;
-    return launch_lm_head_argmax(h, emb, logits, state, tokens_out, tokens_cap, force, n_force,
-                                 V, C, static_cast<hipStream_t>(stream));
+    st = ensure_device();
+    if (st) return st;
+    return launch_lm_head_argmax(h, nullptr, nullptr, 0.f, emb, logits, state, tokens_out,
+                                 tokens_cap, force, n_force, V, C, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

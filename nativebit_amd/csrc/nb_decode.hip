@@ -665,8 +665,17 @@ __device__ __forceinline__ uint32_t orderable(float f) {
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// kNorm: the head's input is RMSNorm(x) * w of the fp32 residual x, formed
+// by every workgroup with add_rmsnorm_kernel's arithmetic (the same
+// per-thread sums over the same 1024 threads, the same reduction and
+// expressions, rounded to bf16), so the logits are those of the two launches
+// add_rmsnorm_kernel + lm_head_argmax_kernel, in one launch.  Otherwise h is
+// that bf16 vector.
+static_assert(kHeadThreads == kNormThreads, "the fused norm repeats add_rmsnorm_kernel's sums");
+template <bool kNorm>
 __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
-    const bf16_bits* __restrict__ h, const bf16_bits* __restrict__ emb, float* __restrict__ logits,
+    const bf16_bits* __restrict__ h, const float* __restrict__ x, const float* __restrict__ nw,
+    float eps, const bf16_bits* __restrict__ emb, float* __restrict__ logits,
     nb_decode_state* __restrict__ st, int32_t* __restrict__ tokens_out, int tokens_cap,
     const int32_t* __restrict__ force, int n_force, int V, int C) {
     typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
@@ -674,7 +683,20 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
     __shared__ unsigned long long wkey[kHeadThreads / 64];
     __shared__ unsigned last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    for (int i = tid; i < C; i += kHeadThreads) hs[i] = bf16_to_f32(h[i]);
+    if constexpr (kNorm) {
+        __shared__ float red[kHeadThreads / 64];
+        float ss = 0.f;
+        for (int i = tid; i < C; i += kHeadThreads) {
+            const float v = x[i];
+            ss += v * v;
+        }
+        const float mean = block_sum(ss, red) / (float)C;
+        const float norm = sqrtf(mean + eps);
+        for (int i = tid; i < C; i += kHeadThreads)
+            hs[i] = bf16_to_f32(f32_to_bf16_rne((x[i] / norm) * nw[i]));
+    } else {
+        for (int i = tid; i < C; i += kHeadThreads) hs[i] = bf16_to_f32(h[i]);
+    }
     __syncthreads();
     unsigned long long best = 0ull;
     const int nwaves = gridDim.x * (kHeadThreads / 64);
@@ -841,14 +863,22 @@ int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t st
     return check_launch("nb_silu_mul");
 }
 
-int launch_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* st,
+int launch_lm_head_argmax(const void* h, const float* x, const float* norm_w, float eps,
+                          const void* emb, float* logits, nb_decode_state* st,
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
                           int V, int C, hipStream_t stream) {
     const int rows_per_block = kHeadRows * (kHeadThreads / 64);
     const int blocks = std::max(1, std::min(device_cu_count(), (V + rows_per_block - 1) / rows_per_block));
-    hipLaunchKernelGGL(lm_head_argmax_kernel, dim3(blocks), dim3(kHeadThreads), 0, stream,
-                       static_cast<const bf16_bits*>(h), static_cast<const bf16_bits*>(emb), logits,
-                       st, tokens_out, tokens_cap, force, n_force, V, C);
+    if (x) {
+        hipLaunchKernelGGL(lm_head_argmax_kernel<true>, dim3(blocks), dim3(kHeadThreads), 0,
+                           stream, nullptr, x, norm_w, eps, static_cast<const bf16_bits*>(emb),
+                           logits, st, tokens_out, tokens_cap, force, n_force, V, C);
+        return check_launch("nb_rmsnorm_lm_head_argmax");
+    }
+    hipLaunchKernelGGL(lm_head_argmax_kernel<false>, dim3(blocks), dim3(kHeadThreads), 0, stream,
+                       static_cast<const bf16_bits*>(h), nullptr, nullptr, 0.f,
+                       static_cast<const bf16_bits*>(emb), logits, st, tokens_out, tokens_cap,
+                       force, n_force, V, C);
     return check_launch("nb_lm_head_argmax");
 }
 

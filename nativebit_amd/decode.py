@@ -7,9 +7,10 @@ synchronises on ``int(logits.argmax())`` every token, generate_torch.py:311).
 
 * ``DecodeEngine``: a token is a fixed sequence of gfx950 launches -- per
   layer q|k|v GEMV (RMSNorm formed in its prologue) -> nb_attention_step ->
-  o GEMV (residual add in its epilogue) -> gate|up GEMV (RMSNorm prologue)
-  -> down GEMV (silu(gate) * up prologue, residual add epilogue), after the
-  embedding lookup and before the final norm and nb_lm_head_argmax --
+  o GEMV (residual add in its epilogue) -> gate|up GEMV (RMSNorm prologue,
+  silu(gate) * up of its row pairs in its epilogue) -> down GEMV (residual
+  add epilogue), after the embedding lookup and before the final norm,
+  head and greedy choice (nb_rmsnorm_lm_head_argmax, one launch) --
   captured once in a HIP graph and replayed.
 * ``PersistentDecodeEngine``: nb_decode_persistent runs many tokens in one
   cooperative launch, the phases of a token separated by grid barriers and
@@ -202,7 +203,7 @@ class DecodeEngine(_DecoderBase):
         self.layer_x = self._z(model.cfg.n_layers, C) if record_layers else None
         z, bf16 = self._z, torch.bfloat16
         self.x = z(C)                # residual stream (fp32)
-        self.h = z(C, dt=bf16)       # normalised embedding row (layer 0) and final norm
+        self.h = z(C, dt=bf16)       # normalised embedding row (layer 0's q|k|v input)
         self.qkv = z(3 * C)
         self.att = z(C, dt=bf16)
         self.act = z(F, dt=bf16)     # silu(gate) * up, the down projection's input
@@ -261,11 +262,11 @@ class DecodeEngine(_DecoderBase):
             g_d.run()                        # x += W_down act
             if self.layer_x is not None:
                 self.layer_x[l].copy_(self.x)
-        ck(lib.nb_add_rmsnorm(_ptr(self.x), None, None, st, _ptr(self.ln_f), _ptr(self.h),
-                              BF, C, self.eps, s))
-        ck(lib.nb_lm_head_argmax(_ptr(self.h), _ptr(self.emb_bf16), _ptr(self.logits), st,
-                                 _ptr(self.tokens), self.max_steps, _ptr(self.force), self.n_force,
-                                 self.V, C, s))
+        # the final norm, the tied head and the greedy choice in one launch
+        ck(lib.nb_rmsnorm_lm_head_argmax(_ptr(self.x), _ptr(self.ln_f), self.eps,
+                                         _ptr(self.emb_bf16), _ptr(self.logits), st,
+                                         _ptr(self.tokens), self.max_steps, _ptr(self.force),
+                                         self.n_force, self.V, C, s))
 
     def step(self):
         """Feed the current token (eagerly, no graph)."""

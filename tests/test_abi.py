@@ -479,6 +479,28 @@ def test_lm_head_validation(kw, status):
     assert _lib.load().nb_lm_head_argmax(*a.values()) == status
 
 
+@pytest.mark.parametrize("kw,status", [
+    (dict(C=100), _lib.NB_EUNSUPPORTED),
+    (dict(V=0), _lib.NB_EUNSUPPORTED),
+    (dict(x=None), _lib.NB_EINVAL),
+    (dict(norm_w=None), _lib.NB_EINVAL),
+    (dict(eps=-1.0), _lib.NB_EINVAL),
+    (dict(eps=float("nan")), _lib.NB_EINVAL),
+    (dict(n_force=3, force=None), _lib.NB_EINVAL),
+    (dict(tokens_cap=4, tokens=None), _lib.NB_EINVAL),
+    (dict(state=None), _lib.NB_EINVAL),
+    (dict(x=FAKE + 2), _lib.NB_EALIGN),
+    (dict(norm_w=FAKE + 2), _lib.NB_EALIGN),
+    (dict(emb=FAKE + 8), _lib.NB_EALIGN),
+])
+def test_rmsnorm_lm_head_validation(kw, status):
+    a = dict(x=FAKE, norm_w=FAKE, eps=1e-6, emb=FAKE, logits=None, state=FAKE, tokens=None,
+             tokens_cap=0, force=None, n_force=0, V=32000, C=2560, stream=None)
+    a.update(kw)
+    assert _lib.load().nb_rmsnorm_lm_head_argmax(*a.values()) == status
+    assert _lib.last_error().startswith("nb_rmsnorm_lm_head_argmax")
+
+
 def test_silu_mul_validation():
     lib = _lib.load()
     assert lib.nb_silu_mul(FAKE, FAKE, _lib.NB_BF16, 0, None) == _lib.NB_EINVAL

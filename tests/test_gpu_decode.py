@@ -183,6 +183,42 @@ def test_lm_head_argmax(dev, V, C):
     assert int(ref.argmax()) == best or float(ref.max() - ref[best]) < 1e-4
 
 
+@pytest.mark.parametrize("V,C", [(32000, 2560), (1000, 256)])
+def test_rmsnorm_lm_head_equals_two_launches(dev, V, C):
+    """nb_rmsnorm_lm_head_argmax (the final norm formed inside the head's
+    launch) gives the logits, token and state of nb_add_rmsnorm followed by
+    nb_lm_head_argmax, bit for bit, with forcing and tokens_out as well."""
+    note(f"rmsnorm + lm_head fused V={V} C={C}")
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(V + C)
+    x = (torch.randn(C, generator=g) * 3).to(dev)
+    w = torch.randn(C, generator=g).to(dev)
+    emb = (torch.randn(V, C, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    force = torch.tensor([11, 12], dtype=torch.int32, device=dev)
+    eps = 1e-6
+    for step, n_force in ((0, 2), (2, 2)):   # a forced step, then a free one
+        st_a = state_tensor(dev, pos=5, token=1, step=step)
+        st_b = state_tensor(dev, pos=5, token=1, step=step)
+        tok_a = torch.full((4,), -1, dtype=torch.int32, device=dev)
+        tok_b = tok_a.clone()
+        h = torch.empty(C, dtype=torch.bfloat16, device=dev)
+        la = torch.empty(V, device=dev)
+        lb = torch.empty(V, device=dev)
+        _lib.check(lib.nb_add_rmsnorm(P(x), None, None, P(st_a), P(w), P(h), _lib.NB_BF16, C, eps,
+                                      stream()))
+        _lib.check(lib.nb_lm_head_argmax(P(h), P(emb), P(la), P(st_a), P(tok_a), 4, P(force),
+                                         n_force, V, C, stream()))
+        _lib.check(lib.nb_rmsnorm_lm_head_argmax(P(x), P(w), eps, P(emb), P(lb), P(st_b), P(tok_b),
+                                                 4, P(force), n_force, V, C, stream()))
+        torch.cuda.synchronize()
+        assert torch.equal(la, lb)
+        assert torch.equal(tok_a, tok_b)
+        sa, sb = read_state(st_a), read_state(st_b)
+        assert (sa.token, sa.pos, sa.step, sa.key, sa.done) == \
+            (sb.token, sb.pos, sb.step, sb.key, sb.done)
+        assert sb.token == (force[step].item() if step < n_force else int(lb.cpu().argmax()))
+
+
 def test_lm_head_ties_and_forcing(dev):
     C, V = 256, 4096
     h = torch.ones(C, dtype=torch.bfloat16)
