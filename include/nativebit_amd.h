@@ -474,23 +474,13 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
  * nb_add_rmsnorm's arithmetic, so the logits are bit for bit those of
  * nb_add_rmsnorm (x unchanged, y and emb NULL) followed by
  * nb_lm_head_argmax.  Same state, tokens and forcing contract.
- * next_emb, next_w, next_x, next_h: all NULL, or all set to have the launch
- * also form the next step's input from the token it hands on (the forced
- * or the chosen one): next_x = next_emb[token] (fp32 [V][C] table, C
- * floats) and next_h = bf16(RMSNorm(next_x) * next_w) with eps -- what
- * nb_add_rmsnorm's embedding form writes for that token, bit for bit.  A
- * forced token outside [0, V) gives NaN rows without a read.  next_x may be
- * x itself.
  * Replaces: the final norm, head and argmax of PackedGPT.forward / benchmark
- *           (inference/generate_torch.py:29-38, 157-159, 311) and, with the
- *           next-step outputs, the next step's embedding lookup and first
- *           norm (generate_torch.py:151, 129).
+ *           (inference/generate_torch.py:29-38, 157-159, 311).
  */
 int nb_rmsnorm_lm_head_argmax(const float* x, const float* norm_w, float eps, const void* emb,
                               float* logits, nb_decode_state* state, int32_t* tokens_out,
                               int tokens_cap, const int32_t* force, int n_force, int V, int C,
-                              const float* next_emb, const float* next_w, float* next_x,
-                              void* next_h, void* stream);
+                              void* stream);
 
 /* ------------------------------------------------------------------------
  * Batched forward pass over T tokens (a prompt fed as one sequence, as

@@ -87,7 +87,7 @@ SIGNATURES = {
     "nb_attention_rows": (_I, [_P, _P, _P, _I, _I, _P, _I, _I, _I, _I, _P]),
     "nb_lm_head_argmax": (_I, [_P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
     "nb_rmsnorm_lm_head_argmax": (_I, [_P, _P, ctypes.c_float, _P, _P, _P, _P, _I, _P, _I, _I,
-                                       _I, _P, _P, _P, _P, _P]),
+                                       _I, _P]),
     "nb_decode_workspace_bytes": (_L, [_P]),
     "nb_decode_persistent": (_I, [_P, _P, _L, _P, _P, _P, _I, _P, _I, _I, _I, _P]),
 }

@@ -802,28 +802,17 @@ int nb_silu_mul(const float* gu, void* act, int act_dtype, int n, void* stream) 
 int nb_rmsnorm_lm_head_argmax(const float* x, const float* norm_w, float eps, const void* emb,
                               float* logits, nb_decode_state* state, int32_t* tokens_out,
                               int tokens_cap, const int32_t* force, int n_force, int V, int C,
-                              const float* next_emb, const float* next_w, float* next_x,
-                              void* next_h, void* stream) {
+                              void* stream) {
     const char* fn = "nb_rmsnorm_lm_head_argmax";
     int st = check_head(fn, x, emb, logits, state, tokens_out, tokens_cap, force, n_force, V, C, 4);
     if (st) return st;
     if (!norm_w) return fail(NB_EINVAL, "%s: norm_w is NULL", fn);
     if (!aligned(norm_w, 4)) return fail(NB_EALIGN, "%s: norm_w not 4-byte aligned", fn);
     if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(NB_EINVAL, "%s: eps=%g", fn, (double)eps);
-    const int n_next = (next_emb != nullptr) + (next_w != nullptr) + (next_x != nullptr) +
-                       (next_h != nullptr);
-    if (n_next != 0 && n_next != 4) {
-        return fail(NB_EINVAL, "%s: next_emb, next_w, next_x, next_h all set or all NULL", fn);
-    }
-    if (n_next && (!aligned(next_emb, 4) || !aligned(next_w, 4) || !aligned(next_x, 4) ||
-                   !aligned(next_h, 2))) {
-        return fail(NB_EALIGN, "%s: misaligned next-step pointer", fn);
-    }
     st = ensure_device();
     if (st) return st;
     return launch_lm_head_argmax(nullptr, x, norm_w, eps, emb, logits, state, tokens_out,
-                                 tokens_cap, force, n_force, V, C, next_emb, next_w, next_x,
-                                 next_h, static_cast<hipStream_t>(stream));
+                                 tokens_cap, force, n_force, V, C, static_cast<hipStream_t>(stream));
 }
 
 int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_state* state,
@@ -835,8 +824,7 @@ int nb_lm_head_argmax(const void* h, const void* emb, float* logits, nb_decode_s
     st = ensure_device();
     if (st) return st;
     return launch_lm_head_argmax(h, nullptr, nullptr, 0.f, emb, logits, state, tokens_out,
-                                 tokens_cap, force, n_force, V, C, nullptr, nullptr, nullptr,
-                                 nullptr, static_cast<hipStream_t>(stream));
+                                 tokens_cap, force, n_force, V, C, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -672,28 +672,19 @@ __device__ __forceinline__ uint32_t orderable(float f) {
 // add_rmsnorm_kernel + lm_head_argmax_kernel, in one launch.  Otherwise h is
 // that bf16 vector.
 static_assert(kHeadThreads == kNormThreads, "the fused norm repeats add_rmsnorm_kernel's sums");
-// With next_x (kNorm only), the workgroup that finishes the choice also
-// forms the next step's input from the token it chose: next_x = the fp32
-// embedding row, next_h = bf16(RMSNorm(next_x) * next_w), with
-// add_rmsnorm_kernel's arithmetic (a token outside [0, V) gives NaN rows
-// without a read).  next_x may be x: every other workgroup has read x
-// before it counts itself done.
 template <bool kNorm>
 __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
-    const bf16_bits* __restrict__ h, const float* x, const float* __restrict__ nw,
+    const bf16_bits* __restrict__ h, const float* __restrict__ x, const float* __restrict__ nw,
     float eps, const bf16_bits* __restrict__ emb, float* __restrict__ logits,
     nb_decode_state* __restrict__ st, int32_t* __restrict__ tokens_out, int tokens_cap,
-    const int32_t* __restrict__ force, int n_force, int V, int C,
-    const float* __restrict__ next_emb, const float* __restrict__ next_w, float* next_x,
-    bf16_bits* __restrict__ next_h) {
+    const int32_t* __restrict__ force, int n_force, int V, int C) {
     typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
     __shared__ __align__(16) float hs[kHeadMaxC];
     __shared__ unsigned long long wkey[kHeadThreads / 64];
     __shared__ unsigned last;
-    __shared__ int next_token;
-    __shared__ float red[kHeadThreads / 64];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if constexpr (kNorm) {
+        __shared__ float red[kHeadThreads / 64];
         float ss = 0.f;
         for (int i = tid; i < C; i += kHeadThreads) {
             const float v = x[i];
@@ -768,39 +759,16 @@ __global__ __launch_bounds__(kHeadThreads) void lm_head_argmax_kernel(
         last = atomicAdd(&st->done, 1u) == gridDim.x - 1 ? 1u : 0u;
     }
     __syncthreads();
-    if (!last) return;
-    if (tid == 0) {
+    if (tid == 0 && last) {
         const unsigned long long key = atomicAdd(&st->key, 0ull);
         const int token = (int)(0xffffffffu - (uint32_t)(key & 0xffffffffull));
         const int step = st->step;
         if (tokens_out && step >= 0 && step < tokens_cap) tokens_out[step] = token;
-        const int next = (step >= 0 && step < n_force) ? force[step] : token;
-        st->token = next;
+        st->token = (step >= 0 && step < n_force) ? force[step] : token;
         st->pos += 1;
         st->step += 1;
         st->key = 0ull;
         st->done = 0u;
-        next_token = next;
-    }
-    if constexpr (kNorm) {
-        if (next_x) {
-            __syncthreads();
-            const int tk = next_token;
-            const bool ok = tk >= 0 && tk < V;
-            const float* row = next_emb + (int64_t)(ok ? tk : 0) * C;
-            float ss = 0.f;
-            for (int i = tid; i < C; i += kHeadThreads) {
-                const float v = ok ? row[i] : __int_as_float(0x7fc00000);
-                next_x[i] = v;
-                ss += v * v;
-            }
-            const float mean = block_sum(ss, red) / (float)C;
-            const float norm = sqrtf(mean + eps);
-            for (int i = tid; i < C; i += kHeadThreads) {
-                const float v = ok ? row[i] : __int_as_float(0x7fc00000);
-                next_h[i] = f32_to_bf16_rne((v / norm) * next_w[i]);
-            }
-        }
     }
 }
 
@@ -898,21 +866,19 @@ int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t st
 int launch_lm_head_argmax(const void* h, const float* x, const float* norm_w, float eps,
                           const void* emb, float* logits, nb_decode_state* st,
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
-                          int V, int C, const float* next_emb, const float* next_w,
-                          float* next_x, void* next_h, hipStream_t stream) {
+                          int V, int C, hipStream_t stream) {
     const int rows_per_block = kHeadRows * (kHeadThreads / 64);
     const int blocks = std::max(1, std::min(device_cu_count(), (V + rows_per_block - 1) / rows_per_block));
     if (x) {
         hipLaunchKernelGGL(lm_head_argmax_kernel<true>, dim3(blocks), dim3(kHeadThreads), 0,
                            stream, nullptr, x, norm_w, eps, static_cast<const bf16_bits*>(emb),
-                           logits, st, tokens_out, tokens_cap, force, n_force, V, C, next_emb,
-                           next_w, next_x, static_cast<bf16_bits*>(next_h));
+                           logits, st, tokens_out, tokens_cap, force, n_force, V, C);
         return check_launch("nb_rmsnorm_lm_head_argmax");
     }
     hipLaunchKernelGGL(lm_head_argmax_kernel<false>, dim3(blocks), dim3(kHeadThreads), 0, stream,
                        static_cast<const bf16_bits*>(h), nullptr, nullptr, 0.f,
                        static_cast<const bf16_bits*>(emb), logits, st, tokens_out, tokens_cap,
-                       force, n_force, V, C, nullptr, nullptr, nullptr, nullptr);
+                       force, n_force, V, C);
     return check_launch("nb_lm_head_argmax");
 }
 

@@ -163,14 +163,11 @@ int launch_attention_step(const float* qkv, float* k_cache, float* v_cache, cons
                           unsigned* done, void* out, int out_dtype, int n_head, int head_dim,
                           int ctx, hipStream_t stream);
 int launch_silu_mul(const float* gu, void* act, int dtype, int n, hipStream_t stream);
-// x != NULL: the head's input is RMSNorm(x) * norm_w (fp32 x), else bf16 h;
-// next_x != NULL (with x): the next step's embedding row and its norm with
-// next_w are formed for the chosen token (next_h bf16).
+// x != NULL: the head's input is RMSNorm(x) * norm_w (fp32 x), else bf16 h.
 int launch_lm_head_argmax(const void* h, const float* x, const float* norm_w, float eps,
                           const void* emb, float* logits, nb_decode_state* st,
                           int32_t* tokens_out, int tokens_cap, const int32_t* force, int n_force,
-                          int V, int C, const float* next_emb, const float* next_w,
-                          float* next_x, void* next_h, hipStream_t stream);
+                          int V, int C, hipStream_t stream);
 int attention_work_floats(int n_head);
 // The allocation-free attention's scratch on the current device (its
 // address from hipGetSymbolAddress, set up once per device).

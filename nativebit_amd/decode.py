@@ -240,18 +240,6 @@ class DecodeEngine(_DecoderBase):
         super().reset(prompt_tokens)
         self.done.zero_()
         self.graph = None  # n_force is baked into the launch
-        self._embed_current()
-
-    def _embed_current(self):
-        """x = embedding[token], h = rmsnorm(x) * ln1 of layer 0 for the
-        state's current token.  Between steps x and h always hold these for
-        the token to be fed: reset() and the prompt pass form them here, and
-        each step's head launch forms them for the token it hands on."""
-        lib = _lib.load()
-        s = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
-        _lib.check(lib.nb_add_rmsnorm(_ptr(self.x), None, _ptr(self.emb_f32), _ptr(self.state_t),
-                                      _ptr(self.norms[0][0]), _ptr(self.h), _lib.NB_BF16, self.C,
-                                      self.eps, s))
 
     def _launch(self):
         lib = _lib.load()
@@ -260,8 +248,9 @@ class DecodeEngine(_DecoderBase):
         st = _ptr(self.state_t)
         C = self.C
         BF = _lib.NB_BF16
-        # x = embedding[token] and h = rmsnorm(x) * ln1 of layer 0 are already
-        # there (see _embed_current)
+        # x = embedding[token], h = rmsnorm(x) * ln1 of layer 0
+        ck(lib.nb_add_rmsnorm(_ptr(self.x), None, _ptr(self.emb_f32), st, _ptr(self.norms[0][0]),
+                              _ptr(self.h), BF, C, self.eps, s))
         for l, (g_qkv, g_o, g_gu, g_d) in enumerate(self.gemvs):
             g_qkv.run()                      # qkv = W_qkv rmsnorm(x)
             ck(lib.nb_attention_step(_ptr(self.qkv), _ptr(self.kc[l]), _ptr(self.vc[l]),
@@ -273,13 +262,11 @@ class DecodeEngine(_DecoderBase):
             g_d.run()                        # x += W_down act
             if self.layer_x is not None:
                 self.layer_x[l].copy_(self.x)
-        # the final norm, the tied head and the greedy choice in one launch,
-        # which also forms x and h of the token it hands on
+        # the final norm, the tied head and the greedy choice in one launch
         ck(lib.nb_rmsnorm_lm_head_argmax(_ptr(self.x), _ptr(self.ln_f), self.eps,
                                          _ptr(self.emb_bf16), _ptr(self.logits), st,
                                          _ptr(self.tokens), self.max_steps, _ptr(self.force),
-                                         self.n_force, self.V, C, _ptr(self.emb_f32),
-                                         _ptr(self.norms[0][0]), _ptr(self.x), _ptr(self.h), s))
+                                         self.n_force, self.V, C, s))
 
     def step(self):
         """Feed the current token (eagerly, no graph)."""
@@ -367,7 +354,7 @@ class DecodeEngine(_DecoderBase):
         ck(lib.nb_lm_head_argmax(_ptr(h[T - 1]), _ptr(self.emb_bf16), _ptr(self.logits),
                                  _ptr(self.state_t), _ptr(self.tokens), self.max_steps,
                                  _ptr(self.force), self.n_force, self.V, C, s))
-        self._embed_current()   # x and h of the first generated token
+        self.x.copy_(x[T - 1])
 
     @torch.no_grad()
     def generate(self, prompt_tokens, n_generate: int, batched_prompt: bool = True) -> list:

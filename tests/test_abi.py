@@ -492,15 +492,10 @@ def test_lm_head_validation(kw, status):
     (dict(x=FAKE + 2), _lib.NB_EALIGN),
     (dict(norm_w=FAKE + 2), _lib.NB_EALIGN),
     (dict(emb=FAKE + 8), _lib.NB_EALIGN),
-    (dict(next_emb=FAKE), _lib.NB_EINVAL),                    # next-step outputs: all or none
-    (dict(next_emb=FAKE, next_w=FAKE, next_x=FAKE), _lib.NB_EINVAL),
-    (dict(next_emb=FAKE, next_w=FAKE, next_x=FAKE + 2, next_h=FAKE), _lib.NB_EALIGN),
-    (dict(next_emb=FAKE, next_w=FAKE, next_x=FAKE, next_h=FAKE + 1), _lib.NB_EALIGN),
 ])
 def test_rmsnorm_lm_head_validation(kw, status):
     a = dict(x=FAKE, norm_w=FAKE, eps=1e-6, emb=FAKE, logits=None, state=FAKE, tokens=None,
-             tokens_cap=0, force=None, n_force=0, V=32000, C=2560, next_emb=None, next_w=None,
-             next_x=None, next_h=None, stream=None)
+             tokens_cap=0, force=None, n_force=0, V=32000, C=2560, stream=None)
     a.update(kw)
     assert _lib.load().nb_rmsnorm_lm_head_argmax(*a.values()) == status
     assert _lib.last_error().startswith("nb_rmsnorm_lm_head_argmax")
